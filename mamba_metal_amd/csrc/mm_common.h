@@ -1,0 +1,120 @@
+// Shared helpers of libmamba_mi355x: element-type traits, 8-wide vector I/O and
+// the thread-local error plumbing behind mm_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/mamba_mi355x.h"
+
+namespace mm {
+
+// ---------------------------------------------------------------------------
+// Host-side error handling.  Every entry point validates on the host first and
+// returns fail(status, ...) before touching HIP; fail() records the message in
+// a thread-local buffer read back by mm_last_error().
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+// Turns the launch status into MM_OK / MM_ERR_HIP.
+int check_launch(const char* what);
+
+inline bool valid_dtype(int32_t dt) { return dt == MM_F32 || dt == MM_F16 || dt == MM_BF16; }
+inline int64_t dtype_size(int32_t dt) { return dt == MM_F32 ? 4 : 2; }
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+inline bool aligned(const void* p, int64_t bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
+}
+
+// ---------------------------------------------------------------------------
+// Device-side element types.  All arithmetic is fp32; T is the storage type.
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef unsigned short ushort8_t __attribute__((ext_vector_type(8)));
+typedef float float8_t __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float bf16_to_f32(unsigned short v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+// Round-to-nearest-even fp32 -> bf16; NaN stays NaN (quiet bit set).
+__device__ __forceinline__ unsigned short f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<unsigned short>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<unsigned short>(u >> 16);
+}
+
+template <int DT>
+struct Ty;
+
+template <>
+struct Ty<MM_F32> {
+  using T = float;
+  using V8 = float8_t;
+  __device__ static __forceinline__ float f(T x) { return x; }
+  __device__ static __forceinline__ T from(float x) { return x; }
+};
+
+template <>
+struct Ty<MM_F16> {
+  using T = _Float16;
+  using V8 = half8_t;
+  __device__ static __forceinline__ float f(T x) { return static_cast<float>(x); }
+  __device__ static __forceinline__ T from(float x) { return static_cast<_Float16>(x); }
+};
+
+template <>
+struct Ty<MM_BF16> {
+  using T = unsigned short;
+  using V8 = ushort8_t;
+  __device__ static __forceinline__ float f(T x) { return bf16_to_f32(x); }
+  __device__ static __forceinline__ T from(float x) { return f32_to_bf16(x); }
+};
+
+template <int DT>
+__device__ __forceinline__ float ld(const void* p, int64_t i) {
+  return Ty<DT>::f(static_cast<const typename Ty<DT>::T*>(p)[i]);
+}
+template <int DT>
+__device__ __forceinline__ void st(void* p, int64_t i, float v) {
+  static_cast<typename Ty<DT>::T*>(p)[i] = Ty<DT>::from(v);
+}
+
+// Fast-math building blocks on the hardware transcendental unit.
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float log2_hw(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float rcp_hw(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// silu(z) = z * sigmoid(z) (selective_scan_chunked.metal:143).
+__device__ __forceinline__ float silu_f(float z) { return z * rcp_hw(1.0f + exp2_hw(-z * kLog2e)); }
+
+// softplus with the reference's cutoff: x <= 20 ? log(1 + exp(x)) : x
+// (selective_scan_chunked.metal:60-65).  log1p is evaluated as
+// log(s) * e / (s - 1) with s = 1 + e (Goldberg's log1p correction) so tiny e
+// keeps full relative precision.
+__device__ __forceinline__ float softplus_cut(float x) {
+  const float e = exp2_hw(x * kLog2e);
+  const float s = 1.0f + e;
+  const float dm = s - 1.0f;
+  const float l = log2_hw(s) * kLn2;
+  const float lp = (dm == 0.0f) ? e : l * (e * rcp_hw(dm));
+  return x <= 20.0f ? lp : x;
+}
+
+// softplus without cutoff: log(1 + exp(x)) = max(x, 0) + log1p(exp(-|x|))
+// (MLX nn.softplus used by MambaBlock.step, mamba_block.py:184).
+__device__ __forceinline__ float softplus_full(float x) {
+  const float e = exp2_hw(-fabsf(x) * kLog2e);
+  const float s = 1.0f + e;
+  const float dm = s - 1.0f;
+  const float l = log2_hw(s) * kLn2;
+  const float lp = (dm == 0.0f) ? e : l * (e * rcp_hw(dm));
+  return fmaxf(x, 0.0f) + lp;
+}
+
+}  // namespace mm

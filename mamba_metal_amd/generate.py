@@ -1,0 +1,193 @@
+"""Autoregressive generation (mamba_metal/generate.py:16-110).
+
+  generate       O(L^2): re-runs the full forward for every new token (the
+                 reference's correctness baseline, generate.py:16-62).
+  generate_fast  one parallel prefill, then O(1) ``model.step`` per token
+                 (generate.py:65-110).  Same signature and string semantics:
+                 greedy when temperature == 0, else sampling from softmax(logits/T);
+                 stops at the tokenizer's EOS; ``on_token`` streams text deltas.
+
+Token-level API for serving and benchmarks (no tokenizer, batch > 1, no EOS):
+  generate_fast_ids  prefill + decode on token ids, greedy or sampled.
+  GraphDecoder       the decode step (embedding -> layers -> head -> argmax)
+                     captured once into a HIP graph and replayed per token, with
+                     the resident conv/SSM states updated in place.
+"""
+
+from __future__ import annotations
+
+from typing import Callable
+
+import torch
+
+
+def _sample(logits: torch.Tensor, temperature: float, generator=None) -> torch.Tensor:
+    if temperature == 0.0:
+        return torch.argmax(logits, dim=-1)
+    probs = torch.softmax(logits.float() / temperature, dim=-1)
+    return torch.multinomial(probs, 1, generator=generator).squeeze(-1)
+
+
+def _encode(tokenizer, prompt: str, device) -> torch.Tensor:
+    ids = tokenizer(prompt, return_tensors="np").input_ids
+    return torch.as_tensor(ids, dtype=torch.long, device=device)
+
+
+def _stream(tokenizer, prompt, generated_ids, prev_text, on_token):
+    new_text = tokenizer.decode(generated_ids, skip_special_tokens=True)
+    delta = new_text[len(prev_text) - len(prompt):]
+    if delta:
+        on_token(delta)
+        return prompt + new_text
+    return prev_text
+
+
+@torch.inference_mode()
+def generate(model, tokenizer, prompt: str, max_new_tokens: int = 50, temperature: float = 0.0,
+             on_token: Callable[[str], None] | None = None) -> str:
+    """O(L^2) generation: full forward over the whole prefix for each token."""
+    device = model.embeddings.weight.device
+    input_ids = _encode(tokenizer, prompt, device)
+    eos = tokenizer.eos_token_id
+    generated_ids: list[int] = []
+    prev_text = prompt
+    for _ in range(max_new_tokens):
+        next_logits = model(input_ids)[:, -1, :]
+        next_id = _sample(next_logits, temperature)
+        next_id_int = int(next_id.reshape(-1)[0].item())
+        if eos is not None and next_id_int == eos:
+            break
+        generated_ids.append(next_id_int)
+        if on_token is not None:
+            prev_text = _stream(tokenizer, prompt, generated_ids, prev_text, on_token)
+        input_ids = torch.cat([input_ids, next_id.reshape(1, 1).to(input_ids.dtype)], dim=1)
+    return prompt + tokenizer.decode(generated_ids, skip_special_tokens=True)
+
+
+@torch.inference_mode()
+def generate_fast(model, tokenizer, prompt: str, max_new_tokens: int = 50,
+                  temperature: float = 0.0,
+                  on_token: Callable[[str], None] | None = None) -> str:
+    """O(L_prompt + n_decode) generation: parallel prefill, then O(1) steps."""
+    device = model.embeddings.weight.device
+    input_ids = _encode(tokenizer, prompt, device)
+    eos = tokenizer.eos_token_id
+    logits, conv_states, ssm_states = model.prefill(input_ids, last_only=True)
+    next_logits = logits[:, -1, :]
+    generated_ids: list[int] = []
+    prev_text = prompt
+    for _ in range(max_new_tokens):
+        next_id = _sample(next_logits, temperature)
+        next_id_int = int(next_id.reshape(-1)[0].item())
+        if eos is not None and next_id_int == eos:
+            break
+        generated_ids.append(next_id_int)
+        if on_token is not None:
+            prev_text = _stream(tokenizer, prompt, generated_ids, prev_text, on_token)
+        ids = torch.tensor([[next_id_int]], dtype=torch.long, device=device)
+        step_logits, conv_states, ssm_states = model.step(ids, conv_states, ssm_states)
+        next_logits = step_logits[:, 0, :]
+    return prompt + tokenizer.decode(generated_ids, skip_special_tokens=True)
+
+
+class GraphDecoder:
+    """Greedy/sampled decode with the whole step captured in one HIP graph.
+
+    ``start(input_ids)`` runs the parallel prefill (its states become the resident
+    decode state) and returns the first token; ``step()`` replays the captured
+    graph -- embedding, every layer's in-place conv/SSM update, the head and
+    argmax -- and returns the next token ids (B,) on the device, with no host
+    sync.  Greedy only when captured (``temperature == 0``); sampling runs eagerly.
+    """
+
+    def __init__(self, model, batch_size: int, use_graph: bool = True):
+        self.model = model
+        self.batch = batch_size
+        self.use_graph = use_graph
+        self.graph = None
+        self.ids = None
+        self.next_ids = None
+        self.convs = None
+        self.ssms = None
+
+    def _eager_step(self):
+        logits, _, _ = self.model.step(self.ids.view(-1, 1), self.convs, self.ssms)
+        return torch.argmax(logits[:, 0, :], dim=-1)
+
+    @torch.inference_mode()
+    def start(self, input_ids: torch.Tensor) -> torch.Tensor:
+        assert input_ids.shape[0] == self.batch
+        logits, convs, ssms = self.model.prefill(input_ids, last_only=True)
+        first = torch.argmax(logits[:, -1, :], dim=-1)
+        if self.convs is None:
+            self.convs, self.ssms = convs, ssms
+            self.ids = first.clone()
+        else:  # keep the captured buffers; copy the new prefill state into them
+            for dst, src in zip(self.convs + self.ssms, convs + ssms):
+                dst.copy_(src)
+            self.ids.copy_(first)
+        if self.use_graph and self.graph is None:
+            self._capture()
+        return first
+
+    def _capture(self):
+        # Warm up on a side stream (lazy library init, hipBLASLt heuristics), then
+        # restore the state the warm-up step advanced.
+        saved = [t.clone() for t in self.convs + self.ssms]
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self._eager_step()
+        torch.cuda.current_stream().wait_stream(s)
+        for dst, src in zip(self.convs + self.ssms, saved):
+            dst.copy_(src)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.next_ids = self._eager_step()
+        # Capturing does not execute; the state is still the prefill state.
+        self.graph = g
+
+    @torch.inference_mode()
+    def step(self) -> torch.Tensor:
+        """Advance every sequence by one token; returns the next ids (B,)."""
+        if self.graph is not None:
+            self.graph.replay()
+            self.ids.copy_(self.next_ids)
+            return self.ids
+        nxt = self._eager_step()
+        self.ids.copy_(nxt)
+        return self.ids
+
+
+@torch.inference_mode()
+def generate_fast_ids(model, input_ids: torch.Tensor, max_new_tokens: int,
+                      temperature: float = 0.0, eos_token_id: int | None = None,
+                      generator: torch.Generator | None = None,
+                      use_graph: bool = False) -> torch.Tensor:
+    """Token-id generate_fast for a (B, L) batch.  Returns (B, max_new_tokens) ids.
+
+    Greedy when temperature == 0.  With eos_token_id set (batch 1 only), stops at
+    EOS as the reference does and returns the ids before it.  use_graph replays
+    a captured HIP graph per step (greedy, no EOS)."""
+    B = input_ids.shape[0]
+    if use_graph and temperature == 0.0 and eos_token_id is None:
+        dec = GraphDecoder(model, B, use_graph=True)
+        toks = [dec.start(input_ids).clone()]
+        for _ in range(max_new_tokens - 1):
+            toks.append(dec.step().clone())
+        return torch.stack(toks[:max_new_tokens], dim=1)
+    logits, convs, ssms = model.prefill(input_ids, last_only=True)
+    nxt = logits[:, -1, :]
+    out = []
+    for i in range(max_new_tokens):
+        tok = _sample(nxt, temperature, generator)
+        if eos_token_id is not None and B == 1 and int(tok[0].item()) == eos_token_id:
+            break
+        out.append(tok)
+        if i + 1 == max_new_tokens:
+            break
+        step_logits, convs, ssms = model.step(tok.view(-1, 1), convs, ssms)
+        nxt = step_logits[:, 0, :]
+    if not out:
+        return torch.empty((B, 0), dtype=torch.long, device=input_ids.device)
+    return torch.stack(out, dim=1)

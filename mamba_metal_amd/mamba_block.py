@@ -1,0 +1,122 @@
+"""One Mamba block on the MI355X kernels (mamba_metal/mamba_block.py:27-198).
+
+Layout (single layer, inference only), as in the reference:
+
+    x (B, L, d_model) -> in_proj -> [x_main, z] -> causal depthwise conv1d -> SiLU
+      -> x_proj -> (dt_pre, B, C) -> dt_proj -> selective scan(A=-exp(A_log), D, z,
+      delta_softplus) -> out_proj
+
+Parameter names and shapes follow the HF checkpoints (and the reference's
+attribute names): in_proj.weight, conv1d.weight (d_inner, 1, d_conv) -- torch/HF
+order, so no transpose is needed (the reference transposes to MLX order,
+load_hf.py:46-50) --, conv1d.bias, x_proj.weight, dt_proj.weight/bias, A_log, D,
+out_proj.weight.  A_log and D stay float32 whatever the model dtype.
+
+Where the reference transposes activations to (B, dim, L) contiguous copies
+before the scan (mamba_block.py:90-100), this block hands the kernel strided
+(B, L, dim) views: the scan reads channel-contiguous tiles directly.
+
+GEMMs (in/x/dt/out projections, tied LM head) run on torch (hipBLASLt); the
+conv, the scan and the decode state updates are libmamba_mi355x kernels.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from mamba_metal_amd.conv1d import causal_conv1d, conv_step
+from mamba_metal_amd.decode import ssm_step
+from mamba_metal_amd.selective_scan import selective_scan_into
+
+
+class MambaBlock(nn.Module):
+    def __init__(self, d_model: int, d_state: int = 16, d_conv: int = 4, expand: int = 2,
+                 dt_rank: int | None = None, device=None, dtype=None):
+        super().__init__()
+        fk = {"device": device, "dtype": dtype}
+        self.d_model = d_model
+        self.d_state = d_state
+        self.d_conv = d_conv
+        self.d_inner = expand * d_model
+        self.dt_rank = math.ceil(d_model / 16) if dt_rank is None else dt_rank
+
+        self.in_proj = nn.Linear(d_model, self.d_inner * 2, bias=False, **fk)
+        self.conv1d = nn.Conv1d(self.d_inner, self.d_inner, kernel_size=d_conv,
+                                groups=self.d_inner, padding=d_conv - 1, bias=True, **fk)
+        self.x_proj = nn.Linear(self.d_inner, self.dt_rank + 2 * d_state, bias=False, **fk)
+        self.dt_proj = nn.Linear(self.dt_rank, self.d_inner, bias=True, **fk)
+        # A = -exp(A_log); init A[d, n] = n + 1 (mamba_block.py:57-63).
+        A_init = torch.arange(1, d_state + 1, dtype=torch.float32, device=device)
+        self.A_log = nn.Parameter(torch.log(A_init).expand(self.d_inner, d_state).contiguous(),
+                                  requires_grad=False)
+        self.D = nn.Parameter(torch.ones(self.d_inner, dtype=torch.float32, device=device),
+                              requires_grad=False)
+        self.out_proj = nn.Linear(self.d_inner, d_model, bias=False, **fk)
+
+    # ------------------------------------------------------------------ helpers
+    def _A(self) -> torch.Tensor:
+        return -torch.exp(self.A_log.float())
+
+    def _split_xdbl(self, x_dbl):
+        r, n = self.dt_rank, self.d_state
+        return x_dbl[..., :r], x_dbl[..., r:r + n], x_dbl[..., r + n:]
+
+    def _mix(self, x, conv_state=None, ssm_state=None):
+        """Shared body of __call__ / prefill.  x: (B, L, d_model)."""
+        Bsz, L, _ = x.shape
+        di = self.d_inner
+        xz = self.in_proj(x)                                   # (B, L, 2*d_inner)
+        x_pre, z = xz[..., :di], xz[..., di:]                  # strided views
+        x_main = causal_conv1d(x_pre, self.conv1d.weight, self.conv1d.bias, apply_silu=True,
+                               conv_state_out=conv_state)      # (B, L, d_inner)
+        x_dbl = self.x_proj(x_main)                            # (B, L, dt_rank + 2N)
+        dt_pre, Bm, Cm = self._split_xdbl(x_dbl)
+        dt = F.linear(dt_pre, self.dt_proj.weight, self.dt_proj.bias)  # (B, L, d_inner)
+        y = torch.empty_like(x_main)
+        selective_scan_into(x_main.transpose(1, 2), dt.transpose(1, 2), self._A(),
+                            Bm.transpose(1, 2), Cm.transpose(1, 2), y.transpose(1, 2),
+                            D=self.D, z=z.transpose(1, 2), delta_softplus=True,
+                            state_out=ssm_state)
+        return self.out_proj(y)
+
+    # --------------------------------------------------------------- public API
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """Full forward without state (mamba_block.py:68-102)."""
+        return self._mix(x)
+
+    def prefill(self, x: torch.Tensor):
+        """Parallel prefill (mamba_block.py:104-153).
+
+        Returns (y (B, L, d_model), conv_state (B, d_inner, d_conv) in x's dtype,
+        ssm_state (B, d_inner, d_state) float32)."""
+        Bsz = x.shape[0]
+        conv_state = torch.empty((Bsz, self.d_inner, self.d_conv), dtype=x.dtype, device=x.device)
+        ssm_state = torch.empty((Bsz, self.d_inner, self.d_state), dtype=torch.float32,
+                                device=x.device)
+        y = self._mix(x, conv_state, ssm_state)
+        return y, conv_state, ssm_state
+
+    def step(self, x_token: torch.Tensor, conv_state: torch.Tensor, ssm_state: torch.Tensor,
+             inplace: bool = True):
+        """O(1) per-token forward (mamba_block.py:155-198).
+
+        x_token (B, 1, d_model).  The resident states are updated IN PLACE by the
+        decode kernels and returned (the reference returns fresh arrays); pass
+        inplace=False to leave the given states untouched."""
+        if not inplace:
+            conv_state = conv_state.clone()
+            ssm_state = ssm_state.clone()
+        di = self.d_inner
+        xz = self.in_proj(x_token[:, 0, :])                    # (B, 2*d_inner)
+        x_main, z = xz[:, :di], xz[:, di:]
+        x_conv = conv_step(conv_state, x_main, self.conv1d.weight, self.conv1d.bias,
+                           apply_silu=True)                    # (B, d_inner)
+        x_dbl = self.x_proj(x_conv)
+        dt_pre, Bm, Cm = self._split_xdbl(x_dbl)
+        dt = F.linear(dt_pre, self.dt_proj.weight, self.dt_proj.bias)
+        y = ssm_step(ssm_state, x_conv, dt, self._A(), Bm, Cm, D=self.D, z=z, dt_softplus=True)
+        return self.out_proj(y)[:, None, :], conv_state, ssm_state

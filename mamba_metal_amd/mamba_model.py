@@ -1,0 +1,144 @@
+"""Full Mamba causal LM on the MI355X kernels (mamba_metal/mamba_model.py:23-127).
+
+Stack of (RMSNorm -> MambaBlock + residual) layers, final RMSNorm and a tied LM
+head (logits = x @ embeddings.weight.T).  Attribute layout mirrors HF's
+``state-spaces/mamba-*-hf`` with the ``backbone.`` prefix stripped:
+
+    embeddings.weight, layers.{i}.norm.weight, layers.{i}.mixer.<X>, norm_f.weight
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+
+from mamba_metal_amd.mamba_block import MambaBlock
+
+
+@dataclass
+class MambaConfig:
+    d_model: int = 768
+    n_layer: int = 24
+    vocab_size: int = 50280
+    d_state: int = 16
+    d_conv: int = 4
+    expand: int = 2
+    dt_rank: int | None = None  # auto = ceil(d_model / 16) if None
+    rms_norm_eps: float = 1e-5
+
+
+class MambaResidualBlock(nn.Module):
+    """Pre-norm + residual wrapper around a MambaBlock (mamba_model.py:35-58)."""
+
+    def __init__(self, cfg: MambaConfig, device=None, dtype=None):
+        super().__init__()
+        self.norm = nn.RMSNorm(cfg.d_model, eps=cfg.rms_norm_eps, device=device, dtype=dtype)
+        self.mixer = MambaBlock(d_model=cfg.d_model, d_state=cfg.d_state, d_conv=cfg.d_conv,
+                                expand=cfg.expand, dt_rank=cfg.dt_rank, device=device, dtype=dtype)
+
+    def forward(self, x):
+        return x + self.mixer(self.norm(x))
+
+    def prefill(self, x):
+        y, conv_state, ssm_state = self.mixer.prefill(self.norm(x))
+        return x + y, conv_state, ssm_state
+
+    def step(self, x_token, conv_state, ssm_state, inplace: bool = True):
+        y, new_conv, new_ssm = self.mixer.step(self.norm(x_token), conv_state, ssm_state,
+                                               inplace=inplace)
+        return x_token + y, new_conv, new_ssm
+
+
+class MambaModel(nn.Module):
+    """Stack of MambaResidualBlocks with a tied LM head (mamba_model.py:61-127)."""
+
+    def __init__(self, cfg: MambaConfig, device=None, dtype=None):
+        super().__init__()
+        self.cfg = cfg
+        self.embeddings = nn.Embedding(cfg.vocab_size, cfg.d_model, device=device, dtype=dtype)
+        self.layers = nn.ModuleList(
+            [MambaResidualBlock(cfg, device=device, dtype=dtype) for _ in range(cfg.n_layer)])
+        self.norm_f = nn.RMSNorm(cfg.d_model, eps=cfg.rms_norm_eps, device=device, dtype=dtype)
+
+    @property
+    def d_inner(self) -> int:
+        return self.cfg.expand * self.cfg.d_model
+
+    def _head(self, x):
+        return self.norm_f(x) @ self.embeddings.weight.T
+
+    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+        """input_ids (B, L) -> logits (B, L, vocab_size)."""
+        x = self.embeddings(input_ids)
+        for layer in self.layers:
+            x = layer(x)
+        return self._head(x)
+
+    def init_state(self, batch_size: int = 1):
+        """Zero conv and SSM states (float32, as mamba_model.py:80-91)."""
+        dev = self.embeddings.weight.device
+        convs = [torch.zeros((batch_size, self.d_inner, self.cfg.d_conv), dtype=torch.float32,
+                             device=dev) for _ in self.layers]
+        ssms = [torch.zeros((batch_size, self.d_inner, self.cfg.d_state), dtype=torch.float32,
+                            device=dev) for _ in self.layers]
+        return convs, ssms
+
+    def prefill(self, input_ids: torch.Tensor, last_only: bool = False):
+        """Process a (B, L) prompt in parallel (mamba_model.py:93-110).
+
+        Returns (logits (B, L, vocab) -- (B, 1, vocab) with last_only=True --,
+        conv_states, ssm_states)."""
+        x = self.embeddings(input_ids)
+        convs, ssms = [], []
+        for layer in self.layers:
+            x, cs, ss = layer.prefill(x)
+            convs.append(cs)
+            ssms.append(ss)
+        if last_only:
+            x = x[:, -1:, :]
+        return self._head(x), convs, ssms
+
+    def step(self, input_ids: torch.Tensor, conv_states, ssm_states, inplace: bool = True):
+        """One new token per sequence (B, 1) -> (logits (B, 1, vocab), states).
+
+        States are updated in place and returned (see MambaBlock.step)."""
+        x = self.embeddings(input_ids.reshape(-1, 1))
+        new_conv, new_ssm = [], []
+        for layer, cs, ss in zip(self.layers, conv_states, ssm_states):
+            x, cs2, ss2 = layer.step(x, cs, ss, inplace=inplace)
+            new_conv.append(cs2)
+            new_ssm.append(ss2)
+        return self._head(x), new_conv, new_ssm
+
+
+@torch.no_grad()
+def init_weights_(model: MambaModel, seed: int = 0, std: float = 0.02,
+                  dt_min: float = 1e-3, dt_max: float = 1e-1) -> MambaModel:
+    """Random init used for the synthetic benchmark models.
+
+    Linear / conv / embedding weights ~ N(0, std); A_log = log(1..d_state);
+    dt_proj.bias = softplus^-1(U(dt_min, dt_max)) = log(expm1(dt)); D = 1;
+    norm weights = 1; conv bias = 0.  Drawn on the model's device from one
+    seeded generator, in a fixed parameter order, so a run is reproducible."""
+    dev = model.embeddings.weight.device
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    for name, p in model.named_parameters():
+        if name.endswith("A_log"):
+            n = p.shape[-1]
+            p.copy_(torch.log(torch.arange(1, n + 1, dtype=torch.float32, device=dev)).expand_as(p))
+        elif name.endswith("mixer.D") or name.endswith("norm.weight") or name == "norm_f.weight":
+            p.fill_(1.0)
+        elif name.endswith("dt_proj.bias"):
+            dt = torch.empty(p.shape, dtype=torch.float32, device=dev)
+            dt.uniform_(dt_min, dt_max, generator=g)
+            p.copy_(torch.log(torch.expm1(dt)).to(p.dtype))
+        elif name.endswith("conv1d.bias"):
+            p.zero_()
+        else:
+            w = torch.empty(p.shape, dtype=torch.float32, device=dev)
+            w.normal_(0.0, std, generator=g)
+            p.copy_(w.to(p.dtype))
+    return model

@@ -1,0 +1,147 @@
+"""selective_scan(): the op API of the selective-scan inference path.
+
+Same signature, shapes, dtype rules and error behaviour as the reference's
+mamba_metal/selective_scan.py:23-80:
+
+  u, delta: (batch, dim, seqlen); A: (dim, dstate); B, C: (batch, dstate, seqlen);
+  D: (dim,) optional; z: (batch, dim, seqlen) optional (gate SiLU(z));
+  delta_softplus applies softplus (cutoff 20) to delta;
+  returns y (u.shape, u.dtype) or (y, ssm_state_out (batch, dim, dstate) float32).
+
+Shape violations raise AssertionError with the reference's conditions
+(selective_scan.py:46-50).  Arithmetic is fp32 inside the HIP kernel for every
+dtype (the reference's generated MSL promotes half loads to float).  Inputs may
+be any strided view -- no contiguous copies are made; the kernel reads strides.
+Mixed dtypes are promoted exactly (to float32) and y is rounded back to u.dtype,
+which is what the reference's float arithmetic + half store does.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from mamba_metal_amd import _lib
+
+TG_SIZE = 1024          # reference constant (selective_scan.py:8); kept for API parity
+MAX_DSTATE = _lib.MAX_DSTATE
+
+
+def _strides3(t):
+    s = t.stride()
+    return (_lib._i64a3)(*s)
+
+
+def _common_dtype(*ts):
+    dts = {t.dtype for t in ts if t is not None}
+    if len(dts) == 1:
+        return dts.pop()
+    return torch.float32
+
+
+def selective_scan_into(u, delta, A, B, C, y, *, D=None, z=None, delta_softplus=False,
+                        state_out=None):
+    """Run the scan writing into a caller-provided y (any strides, shape of u).
+
+    ``state_out`` (batch, dim, dstate) contiguous float32 or None.  Used by the
+    model to pass its (batch, seqlen, dim) buffers as transposed views."""
+    lib = _lib.load()
+    dev = _lib.require_cuda(u, delta, A, B, C, D, z, y, state_out)
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
+    xdt = _common_dtype(u, delta, z)
+    if xdt != u.dtype or y.dtype != xdt:
+        raise TypeError("selective_scan_into needs u, delta, z and y of one dtype")
+    bcdt = _common_dtype(B, C)
+    if B.dtype != bcdt:
+        B = B.float()
+    if C.dtype != bcdt:
+        C = C.float()
+    A = A if A.dtype == torch.float32 else A.float()
+    if D is not None and D.dtype != torch.float32:
+        D = D.float()
+    if state_out is not None:
+        assert state_out.shape == (batch, dim, dstate) and state_out.is_contiguous()
+        assert state_out.dtype == torch.float32
+
+    ws_bytes = lib.mm_selective_scan_workspace_size(batch, dstate, seqlen)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
+
+    p = _lib.ScanParams()
+    p.u, p.delta, p.A, p.B, p.C = u.data_ptr(), delta.data_ptr(), A.data_ptr(), B.data_ptr(), C.data_ptr()
+    p.D = _lib.ptr(D)
+    p.z = _lib.ptr(z)
+    p.y = y.data_ptr()
+    p.state_out = _lib.ptr(state_out)
+    p.workspace = _lib.ptr(ws)
+    p.workspace_bytes = ws_bytes
+    p.batch, p.dim, p.dstate, p.seqlen = batch, dim, dstate, seqlen
+    p.u_stride = _strides3(u)
+    p.delta_stride = _strides3(delta)
+    p.z_stride = _strides3(z) if z is not None else (_lib._i64a3)(0, 0, 0)
+    p.y_stride = _strides3(y)
+    p.B_stride = _strides3(B)
+    p.C_stride = _strides3(C)
+    p.A_stride = (_lib._i64a2)(*A.stride())
+    p.D_stride = D.stride(0) if D is not None else 0
+    p.x_dtype = _lib.dtype_code(xdt)
+    p.bc_dtype = _lib.dtype_code(bcdt)
+    p.delta_softplus = 1 if delta_softplus else 0
+    p.reserved = 0
+    with torch.cuda.device(dev):
+        st = lib.mm_selective_scan_fwd_strided(p, _lib.stream_of(dev))
+    _lib.check(st, "mm_selective_scan_fwd_strided")
+    return y
+
+
+def selective_scan(
+    u: torch.Tensor,
+    delta: torch.Tensor,
+    A: torch.Tensor,
+    B: torch.Tensor,
+    C: torch.Tensor,
+    *,
+    D: torch.Tensor | None = None,
+    z: torch.Tensor | None = None,
+    delta_softplus: bool = False,
+    return_state: bool = False,
+):
+    """Mamba selective scan with optional D / z / softplus (see module docstring)."""
+    batch, dim, seqlen = u.shape
+    _, dstate = A.shape
+    if not delta.shape == u.shape:
+        raise AssertionError(f"delta.shape {tuple(delta.shape)} != u.shape {tuple(u.shape)}")
+    if not (B.shape == (batch, dstate, seqlen) == C.shape):
+        raise AssertionError(
+            f"B {tuple(B.shape)} and C {tuple(C.shape)} must both be {(batch, dstate, seqlen)}")
+    if not dstate <= MAX_DSTATE:
+        raise AssertionError(f"dstate={dstate} > MAX_DSTATE={MAX_DSTATE}")
+    if z is not None and z.shape != u.shape:
+        raise AssertionError(f"z.shape {tuple(z.shape)} != u.shape {tuple(u.shape)}")
+    if D is not None and D.shape != (dim,):
+        raise AssertionError(f"D.shape {tuple(D.shape)} != ({dim},)")
+    _lib.require_cuda(u, delta, A, B, C, D, z)
+
+    if batch * dim * seqlen == 0:
+        # Nothing to scan; h stays at its zero initial value (the reference's carry init).
+        y = torch.empty((batch, dim, seqlen), dtype=u.dtype, device=u.device)
+        if return_state:
+            return y, torch.zeros((batch, dim, dstate), dtype=torch.float32, device=u.device)
+        return y
+
+    out_dtype = u.dtype
+    xdt = _common_dtype(u, delta, z)
+    _lib.dtype_code(xdt)
+    uu = u if u.dtype == xdt else u.to(xdt)
+    dd = delta if delta.dtype == xdt else delta.to(xdt)
+    zz = z if (z is None or z.dtype == xdt) else z.to(xdt)
+
+    y = torch.empty((batch, dim, seqlen), dtype=xdt, device=u.device)
+    state = torch.empty((batch, dim, dstate), dtype=torch.float32, device=u.device) \
+        if return_state else None
+    selective_scan_into(uu, dd, A, B, C, y, D=D, z=zz, delta_softplus=delta_softplus,
+                        state_out=state)
+    if y.dtype != out_dtype:
+        y = y.to(out_dtype)
+    if return_state:
+        return y, state
+    return y

@@ -1,0 +1,155 @@
+"""CPU tests of the C ABI boundary (no GPU needed).
+
+  - libmamba_mi355x.so loads next to torch's HIP runtime and exports every
+    function include/mamba_mi355x.h declares;
+  - the ctypes mirror of mm_scan_params matches the C layout (offsets compiled
+    from the header with gcc);
+  - host-only validation rejects invalid arguments with the documented status
+    BEFORE any HIP call (these calls never reach the device).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from mamba_metal_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "mamba_mi355x.h"
+FAKE = 0x1000  # never dereferenced: every call below fails validation first
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mm_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 10, names
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in {HEADER.name} but not exported"
+    assert set(names) == set(_lib.EXPORTED), "python binding and header disagree"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (mm_[a-z0-9_]+)$", out, flags=re.M))
+    assert set(names) <= exported
+
+
+def test_version_and_status_names(lib):
+    assert lib.mm_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.mm_status_name(0) == b"MM_OK"
+    assert lib.mm_status_name(-3) == b"MM_ERR_DSTATE"
+    assert lib.mm_status_name(-99) == b"MM_ERR_UNKNOWN"
+
+
+def test_single_hip_runtime_mapped(lib):
+    assert len(_lib._hip_runtimes_mapped()) == 1
+
+
+def test_scan_params_layout_matches_header(tmp_path):
+    fields = [f for f, _ in _lib.ScanParams._fields_]
+    src = tmp_path / "off.c"
+    body = "\n".join(f'printf("{f} %zu\\n", offsetof(mm_scan_params, {f}));' for f in fields)
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "mamba_mi355x.h"\n'
+                   'int main(void){\n' + body + '\nprintf("sizeof %zu\\n", sizeof(mm_scan_params));'
+                   "return 0;}\n")
+    exe = tmp_path / "off"
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                 check=True).stdout.splitlines())
+    for f in fields:
+        assert int(got[f]) == getattr(_lib.ScanParams, f).offset, f
+    assert int(got["sizeof"]) == ctypes.sizeof(_lib.ScanParams)
+
+
+def _scan(lib, **over):
+    args = dict(u=FAKE, delta=FAKE, A=FAKE, B=FAKE, C=FAKE, D=None, z=None, y=FAKE, state=None,
+                batch=1, dim=16, dstate=16, seqlen=64, x_dtype=0, bc_dtype=0, softplus=0,
+                ws=FAKE, ws_bytes=1 << 30)
+    args.update(over)
+    return lib.mm_selective_scan_fwd(
+        args["u"], args["delta"], args["A"], args["B"], args["C"], args["D"], args["z"],
+        args["y"], args["state"], args["batch"], args["dim"], args["dstate"], args["seqlen"],
+        args["x_dtype"], args["bc_dtype"], args["softplus"], args["ws"], args["ws_bytes"], None)
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(u=None), _lib.ERR_NULL_POINTER),
+    (dict(B=None), _lib.ERR_NULL_POINTER),
+    (dict(y=None), _lib.ERR_NULL_POINTER),
+    (dict(dstate=65), _lib.ERR_DSTATE),
+    (dict(dstate=0), _lib.ERR_DSTATE),
+    (dict(batch=-1), _lib.ERR_SHAPE),
+    (dict(seqlen=-5), _lib.ERR_SHAPE),
+    (dict(batch=70000), _lib.ERR_SHAPE),
+    (dict(x_dtype=7), _lib.ERR_DTYPE),
+    (dict(bc_dtype=-1), _lib.ERR_DTYPE),
+    (dict(ws=None), _lib.ERR_WORKSPACE),
+    (dict(ws_bytes=16), _lib.ERR_WORKSPACE),
+])
+def test_scan_validation_errors(lib, over, status):
+    st = _scan(lib, **over)
+    assert st == status
+    msg = lib.mm_last_error().decode()
+    assert msg.startswith(lib.mm_status_name(status).decode())
+
+
+def test_workspace_size(lib):
+    # batch * 4 groups * round_up(seqlen, 32) * 2 * states-per-lane floats
+    assert lib.mm_selective_scan_workspace_size(4, 16, 32768) == 4 * 4 * 32768 * 2 * 4 * 4
+    assert lib.mm_selective_scan_workspace_size(1, 16, 1) == 1 * 4 * 32 * 8 * 4
+    assert lib.mm_selective_scan_workspace_size(1, 64, 100) == 4 * 128 * 32 * 4
+    assert lib.mm_selective_scan_workspace_size(1, 65, 100) == 0
+    assert lib.mm_selective_scan_workspace_size(0, 16, 100) == 0
+
+
+def test_strided_null_params(lib):
+    assert lib.mm_selective_scan_fwd_strided(None, None) == _lib.ERR_NULL_POINTER
+    p = _lib.ScanParams()
+    p.u = p.delta = p.A = p.B = p.C = p.y = FAKE
+    p.batch, p.dim, p.dstate, p.seqlen = 1, 4, 4, 8
+    p.workspace, p.workspace_bytes = FAKE, 1 << 20
+    p.reserved = 1
+    assert lib.mm_selective_scan_fwd_strided(ctypes.byref(p), None) == _lib.ERR_LAYOUT
+
+
+def test_conv_and_decode_validation(lib):
+    s3 = (_lib._i64a3)(1, 1, 1)
+    s2 = (_lib._i64a2)(4, 1)
+    assert lib.mm_causal_conv1d_fwd(None, FAKE, None, FAKE, None, 1, 8, 8, 4, s3, s3, s2, 1, 1, 1,
+                                    None) == _lib.ERR_NULL_POINTER
+    assert lib.mm_causal_conv1d_fwd(FAKE, FAKE, None, FAKE, None, 1, 8, 8, 9, s3, s3, s2, 1, 1, 1,
+                                    None) == _lib.ERR_SHAPE
+    assert lib.mm_causal_conv1d_fwd(FAKE, FAKE, None, FAKE, None, 1, 8, 8, 4, s3, s3, s2, 5, 1, 1,
+                                    None) == _lib.ERR_DTYPE
+    assert lib.mm_decode_conv_step(FAKE, FAKE, FAKE, None, FAKE, 1, 8, 0, 8, 8, s2, 1, 1, 1, 1,
+                                   None) == _lib.ERR_SHAPE
+    assert lib.mm_decode_ssm_step(FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, None, None, FAKE,
+                                  1, 8, 65, 8, 8, 16, 16, 8, 8, 1, 1, None) == _lib.ERR_DSTATE
+    assert lib.mm_decode_ssm_step(FAKE + 4, FAKE, FAKE, None, FAKE, FAKE, FAKE, None, None, FAKE,
+                                  1, 8, 16, 8, 8, 16, 16, 8, 8, 1, 1, None) == _lib.ERR_LAYOUT
+    assert lib.mm_pair_scan(FAKE, FAKE, None, FAKE, -1, None) == _lib.ERR_SHAPE
+    assert lib.mm_pair_scan(None, FAKE, None, FAKE, 4, None) == _lib.ERR_NULL_POINTER
+
+
+def test_zero_sizes_are_noops(lib):
+    # Nothing to do -> MM_OK without touching the (fake) pointers or the device.
+    assert _scan(lib, batch=0) == _lib.OK
+    assert _scan(lib, dim=0) == _lib.OK
+    s3 = (_lib._i64a3)(1, 1, 1)
+    s2 = (_lib._i64a2)(4, 1)
+    assert lib.mm_causal_conv1d_fwd(FAKE, FAKE, None, FAKE, None, 1, 0, 8, 4, s3, s3, s2, 1, 1, 1,
+                                    None) == _lib.OK
+    assert lib.mm_pair_scan(FAKE, FAKE, None, FAKE, 0, None) == _lib.OK
