@@ -203,7 +203,11 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only-scan", action="store_true",
+                    help="config-4 scan only (the command the committed rocprof summaries use)")
     args = ap.parse_args()
+    if args.only_scan:
+        args.no_extra = args.no_decode = args.no_cpu = True
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); the scan shards over "
               "(batch, channel) with no exchange -- see DESIGN.md", file=sys.stderr)

@@ -73,8 +73,11 @@ const char* mm_status_name(int status);
  * selective_scan.py:52-60).
  */
 
-/* Device workspace (bytes) the scan needs for (batch, dstate, seqlen). */
-size_t mm_selective_scan_workspace_size(int64_t batch, int64_t dstate, int64_t seqlen);
+/* Device workspace (bytes) the scan needs: B/C repacked as fp32 for the kernel,
+ * the per-(channel block) state carried between time segments, and the work-queue
+ * counter and flags.  Depends on dim through the number of 64-channel blocks. */
+size_t mm_selective_scan_workspace_size(int64_t batch, int64_t dim, int64_t dstate,
+                                        int64_t seqlen);
 
 /* Reference-shaped entry point: every tensor row-major contiguous exactly as
  * selective_scan.py:36-44 lays them out -- u, delta, z, y (batch, dim, seqlen);
@@ -102,7 +105,7 @@ typedef struct mm_scan_params {
   const void* z;            /* (batch, dim, seqlen), x_dtype; NULL = no gate      */
   void* y;                  /* (batch, dim, seqlen), x_dtype, output              */
   float* state_out;         /* (batch, dim, dstate) contiguous fp32; NULL = skip */
-  void* workspace;          /* >= mm_selective_scan_workspace_size() bytes       */
+  void* workspace;          /* >= mm_selective_scan_workspace_size() bytes, 256-byte aligned */
   size_t workspace_bytes;
   int64_t batch, dim, dstate, seqlen;
   int64_t u_stride[3];      /* element strides in (batch, dim, time) order       */

@@ -63,7 +63,7 @@ _SIGNATURES = {
     "mm_abi_version": ([], ctypes.c_int),
     "mm_last_error": ([], ctypes.c_char_p),
     "mm_status_name": ([ctypes.c_int], ctypes.c_char_p),
-    "mm_selective_scan_workspace_size": ([_i64, _i64, _i64], _sz),
+    "mm_selective_scan_workspace_size": ([_i64, _i64, _i64, _i64], _sz),
     "mm_selective_scan_fwd": (
         [_vp] * 9 + [_i64] * 4 + [_i32, _i32, _i32, _vp, _sz, _vp], ctypes.c_int),
     "mm_selective_scan_fwd_strided": ([ctypes.POINTER(ScanParams), _vp], ctypes.c_int),

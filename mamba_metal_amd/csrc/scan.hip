@@ -3,318 +3,485 @@
 // Semantics follow mamba_metal/kernels/selective_scan_chunked.metal:28-155
 // (softplus cutoff :60-65, discretisation :78-79, y accumulation :126-128,
 // SiLU(z) gate :140-144, final state :151-155) and the op wrapper
-// mamba_metal/selective_scan.py:23-80.  The decomposition is this library's own:
+// mamba_metal/selective_scan.py:23-80.  The decomposition is this library's own.
 //
-//   * One workgroup = 64 channels (one per lane) of one batch row x 4 state
-//     groups (one per wave).  Each lane walks time SEQUENTIALLY and keeps its
-//     SPL = ceil(dstate/4) states in fp32 registers, so the recurrence costs
-//     exactly one exp2 + four VALU ops per (channel, state, step) and there is
-//     no parallel-scan overhead at all: parallelism comes from the
-//     batch*dim*4 independent (channel, state-group) recurrences.
-//   * B and C are identical for every channel of a batch row.  A tiny pack
-//     kernel rewrites them once into fp32 [batch][group][time][B(SPL),C(SPL)]
-//     in the workspace, so inside the scan loop they are wave-uniform
-//     addresses: the compiler fetches them with s_load into SGPRs and the
-//     VALU reads them as scalar operands (no LDS, no VGPRs, no per-lane loads).
-//   * Per time tile (32 steps) the whole workgroup runs a prologue over the
-//     64x32 (channel, time) elements -- coalesced 16-byte loads of u, delta, z
-//     along whichever axis is contiguous, softplus, delta*u, D*u, SiLU(z) --
-//     and stores delta' and delta'*u to LDS; the 4 waves then scan; then the
-//     epilogue sums the 4 per-group partial y from LDS, adds D*u, applies the
-//     gate and stores y with 16-byte stores.  The next tile's raw loads are
-//     issued before the scan so HBM latency hides under the VALU work.
-//   * The running state never leaves registers between tiles (the reference
-//     keeps a threadgroup-memory carry, selective_scan_chunked.metal:37-47).
+// Work decomposition
+//   * A workgroup owns a block of 64 channels (one per lane) of one batch row and
+//     G waves; wave g owns states [g*SPL, (g+1)*SPL) of every channel (G*SPL >= dstate).
+//     Each lane walks time SEQUENTIALLY with its SPL states in fp32 registers: the
+//     recurrence costs one exp2 and four VALU ops per (channel, state, step), with no
+//     parallel-scan overhead.
+//   * Time is cut into segments.  Work units = (channel block, segment), numbered
+//     segment-major.  A persistent grid (one or two workgroups per CU) claims units
+//     from an atomic ticket counter; a unit waits for its predecessor segment's flag,
+//     reads the carried fp32 state, scans its segment, writes the state and raises its
+//     own flag.  Every predecessor was claimed earlier by a resident workgroup, so the
+//     wait always ends; the spin is bounded anyway.  This balances 320 channel blocks
+//     (config 4) over 256 CUs, which a one-block-per-workgroup grid cannot.
+//   * Per 32-step tile the workgroup runs a prologue over the 64 x 32 (channel, time)
+//     elements -- coalesced vector loads of u, delta, z along whichever axis is
+//     contiguous, softplus, delta*u, D*u, SiLU(z) -- and stages delta', delta'*u and
+//     the tile's B/C (packed fp32 by a small kernel) in LDS; the G waves scan with
+//     LDS reads software-pipelined one 4-step group ahead; the epilogue sums the G
+//     partial y's, adds D*u, gates and stores with vector stores.  The next tile's
+//     global loads are issued before the scan so HBM latency hides under VALU work.
+//   * Exponentials run in the log2 domain: delta2 = delta' * log2(e) so exp(delta'*A)
+//     = exp2(delta2 * A); the packed B carries the matching factor ln(2).
+#include <algorithm>
+
 #include "mm_common.h"
 
 namespace mm {
 namespace scan {
 
-constexpr int kCPW = 64;                 // channels per workgroup (lanes per wave)
-constexpr int kGroups = 4;               // state groups = waves per workgroup
-constexpr int kThreads = kCPW * kGroups; // 256
-constexpr int kT = 32;                   // timesteps per tile
-constexpr int kTP = kT + 4;              // padded LDS row length (floats)
-constexpr int kVec = 8;                  // elements per prologue/epilogue vector
-static_assert(kCPW * kT / kVec == kThreads, "one vector per thread per tile");
+constexpr int kCPW = 64;     // channels per workgroup (lanes per wave)
+constexpr int kT = 32;       // timesteps per tile
+constexpr int kTP = kT + 4;  // padded LDS row length (floats)
+constexpr int kSpinLimit = 1 << 26;
 
 enum Layout { kTimeContig = 0, kChanContig = 1 };
 
 struct Params {
-  const void* u;
-  const void* delta;
-  const void* z;
-  void* y;
   const float* A;
   const float* D;
-  float* state_out;
-  const float* bc;  // packed B/C
-  int64_t dim, dstate, seqlen, Lp, ntiles;
+  int64_t dim, dstate, seqlen, Lp;
+  int64_t nblk_d;     // channel blocks per batch row
+  int64_t ncb;        // channel blocks in total (batch * nblk_d)
+  int64_t seg_tiles;  // tiles per segment
+  int64_t nseg;       // segments per chain
+  int64_t nunits;     // ncb * nseg
   int64_t us0, us1, us2, ds0, ds1, ds2, zs0, zs1, zs2, ys0, ys1, ys2;
   int64_t As0, As1, Ds;
   int32_t softplus;
   int32_t vec_ok;
 };
 
-inline int spl_for(int64_t dstate) {
-  return dstate <= 4 ? 1 : dstate <= 8 ? 2 : dstate <= 16 ? 4 : dstate <= 32 ? 8 : 16;
+// Workspace: [ctl: ticket counter + error word][flags: ncb ints][carry: ncb*16*64*... floats][bc]
+struct WsLayout {
+  size_t flags, carry, bc, total;
+};
+
+inline WsLayout ws_layout(int64_t batch, int64_t dim, int64_t groups, int64_t spl, int64_t seqlen) {
+  const int64_t ncb = batch * ceil_div(dim, kCPW);
+  WsLayout w;
+  w.flags = 256;
+  w.carry = static_cast<size_t>(round_up(w.flags + 4 * ncb, 256));
+  w.bc = static_cast<size_t>(round_up(w.carry + 4 * ncb * groups * spl * kCPW, 256));
+  w.total = w.bc + static_cast<size_t>(4 * batch * groups * round_up(seqlen, kT) * 2 * spl);
+  return w;
+}
+
+inline void pick_shape(int64_t dstate, int* groups, int* spl) {
+  // 8 waves x 2 states for dstate <= 16 (enough waves per CU to hide the exp and LDS
+  // latency at one workgroup per CU); 4 waves x SPL above.
+  if (dstate <= 16) {
+    *groups = 8;
+    *spl = dstate <= 8 ? 1 : 2;
+  } else {
+    *groups = 4;
+    *spl = dstate <= 32 ? 8 : 16;
+  }
 }
 
 // ---------------------------------------------------------------------------
-// B/C pack: bc[((b*4 + g)*Lp + t)*2*SPL + k]       = B[b, g*SPL + k, t]
-//           bc[((b*4 + g)*Lp + t)*2*SPL + SPL + k] = C[b, g*SPL + k, t]
-// zero for padded states (n >= dstate) and padded steps (t >= seqlen).
-template <int DT, int SPL>
+// B/C pack: bc[((b*G + g)*Lp + t)*2*SPL + k]       = ln2 * B[b, g*SPL + k, t]
+//           bc[((b*G + g)*Lp + t)*2*SPL + SPL + k] = C[b, g*SPL + k, t]
+// zero for padded states and steps.  Also clears the ticket counter and flags.
+template <int DT, int SPL, int G>
 __global__ __launch_bounds__(256) void pack_bc_kernel(const void* __restrict__ B,
                                                       const void* __restrict__ C,
-                                                      float* __restrict__ bc, int64_t batch,
-                                                      int64_t dstate, int64_t seqlen, int64_t Lp,
-                                                      int64_t Bs0, int64_t Bs1, int64_t Bs2,
-                                                      int64_t Cs0, int64_t Cs1, int64_t Cs2) {
-  const int64_t total = batch * (kGroups * SPL) * Lp;
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+                                                      float* __restrict__ bc,
+                                                      int* __restrict__ ctl, int64_t nctl,
+                                                      int64_t batch, int64_t dstate,
+                                                      int64_t seqlen, int64_t Lp, int64_t Bs0,
+                                                      int64_t Bs1, int64_t Bs2, int64_t Cs0,
+                                                      int64_t Cs1, int64_t Cs2) {
+  const int64_t gid = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = gid; i < nctl; i += stride) ctl[i] = 0;
+  const int64_t total = batch * (G * SPL) * Lp;
+  for (int64_t i = gid; i < total; i += stride) {
     const int64_t t = i % Lp;
-    const int64_t n = (i / Lp) % (kGroups * SPL);
-    const int64_t b = i / (Lp * kGroups * SPL);
+    const int64_t n = (i / Lp) % (G * SPL);
+    const int64_t b = i / (Lp * G * SPL);
     const bool ok = n < dstate && t < seqlen;
-    const float bv = ok ? ld<DT>(B, b * Bs0 + n * Bs1 + t * Bs2) : 0.0f;
+    const float bv = ok ? ld<DT>(B, b * Bs0 + n * Bs1 + t * Bs2) * kLn2 : 0.0f;
     const float cv = ok ? ld<DT>(C, b * Cs0 + n * Cs1 + t * Cs2) : 0.0f;
     const int64_t g = n / SPL, k = n % SPL;
-    float* o = bc + ((b * kGroups + g) * Lp + t) * (2 * SPL);
+    float* o = bc + ((b * G + g) * Lp + t) * (2 * SPL);
     o[k] = bv;
     o[SPL + k] = cv;
   }
 }
 
-// ---------------------------------------------------------------------------
-template <int DT, int LAYOUT, int SPL>
-__global__ __launch_bounds__(kThreads) void scan_kernel(const Params p, const void* __restrict__ u_,
-                                                        const void* __restrict__ delta_,
-                                                        const void* __restrict__ z_,
-                                                        void* __restrict__ y_,
-                                                        const float* __restrict__ bc_,
-                                                        float* __restrict__ state_out_) {
+template <int DT, int N>
+struct Vec;
+template <int DT>
+struct Vec<DT, 8> {
   using T = typename Ty<DT>::T;
-  using V8 = typename Ty<DT>::V8;
+  typedef T type __attribute__((ext_vector_type(8)));
+};
+template <int DT>
+struct Vec<DT, 4> {
+  using T = typename Ty<DT>::T;
+  typedef T type __attribute__((ext_vector_type(4)));
+};
+template <int DT>
+struct Vec<DT, 2> {
+  using T = typename Ty<DT>::T;
+  typedef T type __attribute__((ext_vector_type(2)));
+};
 
-  __shared__ __attribute__((aligned(16))) float s_dt[kCPW][kTP];        // delta'
-  __shared__ __attribute__((aligned(16))) float s_du[kCPW][kTP];        // delta' * u
-  __shared__ __attribute__((aligned(16))) float s_y[kGroups][kCPW][kTP];// partial y
+// delta2 = softplus(x) * log2(e).  fp32 inputs keep log1p accuracy; fp16/bf16 inputs
+// (whose own rounding is 2^-11 / 2^-8) use log2(1 + 2^m) directly.
+template <int DT>
+__device__ __forceinline__ float softplus_log2(float x) {
+  const float m = x * kLog2e;
+  if (DT == MM_F32) return softplus_cut(x) * kLog2e;
+  const float l = log2_hw(1.0f + exp2_hw(m));
+  return x <= 20.0f ? l : m;
+}
+
+// ---------------------------------------------------------------------------
+template <int DT, int LAYOUT, int SPL, int G>
+__global__ __launch_bounds__(kCPW * G) void scan_kernel(
+    const Params p, const void* __restrict__ u_, const void* __restrict__ delta_,
+    const void* __restrict__ z_, void* __restrict__ y_, const float* __restrict__ bc_,
+    float* __restrict__ state_out_, int* __restrict__ ctl_, float* __restrict__ carry_) {
+  using T = typename Ty<DT>::T;
+  constexpr int NT = kCPW * G;
+  constexpr int EPT = kCPW * kT / NT;  // elements per thread per tile
+  static_assert(EPT == 8 || EPT == 4 || EPT == 2, "tile split");
+  using VE = typename Vec<DT, EPT>::type;
+  constexpr int TPC = kT / EPT;        // threads per channel (time-contiguous mapping)
+  constexpr int BCF = G * kT * 2 * SPL;  // floats of B/C per tile
+  constexpr int BCV = BCF / 4;
+  constexpr int BCPT = (BCV + NT - 1) / NT;
+
+  __shared__ __attribute__((aligned(16))) float s_dt[kCPW][kTP];    // delta2
+  __shared__ __attribute__((aligned(16))) float s_du[kCPW][kTP];    // delta2 * u
+  __shared__ __attribute__((aligned(16))) float s_y[G][kCPW][kTP];  // partial y
+  __shared__ __attribute__((aligned(16))) float s_bc[G][kT][2 * SPL];
+  __shared__ int s_ticket;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int g = __builtin_amdgcn_readfirstlane(tid >> 6);  // state group (wave-uniform)
-  const int64_t b = blockIdx.y;
-  const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kCPW;
+  const int g = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool has_z = z_ != nullptr;
 
-  // ---- per-lane recurrence constants ----
-  float A2[SPL], h[SPL];
-  {
-    const int64_t d = d0 + lane;
-#pragma unroll
-    for (int k = 0; k < SPL; ++k) {
-      const int64_t n = static_cast<int64_t>(g) * SPL + k;
-      A2[k] = (d < p.dim && n < p.dstate) ? p.A[d * p.As0 + n * p.As1] * kLog2e : 0.0f;
-      h[k] = 0.0f;
-    }
-  }
-
-  // ---- this thread's prologue/epilogue vector: 8 (channel, time) elements ----
-  // kTimeContig: channel vc, times vt..vt+7.  kChanContig: channels vc..vc+7, time vt.
-  const int vc = (LAYOUT == kTimeContig) ? (tid >> 2) : ((tid >> 5) * kVec);
-  const int vt = (LAYOUT == kTimeContig) ? ((tid & 3) * kVec) : (tid & 31);
+  // Element ownership for prologue/epilogue.
+  const int vc = (LAYOUT == kTimeContig) ? (tid / TPC) : ((tid / kT) * EPT);
+  const int vt = (LAYOUT == kTimeContig) ? ((tid % TPC) * EPT) : (tid % kT);
   auto ec = [&](int j) { return (LAYOUT == kTimeContig) ? vc : vc + j; };
   auto et = [&](int j) { return (LAYOUT == kTimeContig) ? vt + j : vt; };
 
-  const bool has_z = z_ != nullptr;
-  float Dv[kVec];
-#pragma unroll
-  for (int j = 0; j < kVec; ++j) {
-    const int64_t d = d0 + ec(j);
-    Dv[j] = (p.D != nullptr && d < p.dim) ? p.D[d * p.Ds] : 0.0f;
-  }
-
-  V8 ru, rd, rz;
-  auto load_raw = [&](int64_t t0) {
-    if (p.vec_ok) {
-      // The 8 elements are contiguous: one 16-byte (fp16/bf16) or 32-byte (fp32) load.
-      const bool in = (d0 + vc < p.dim) && (t0 + vt < p.seqlen);
-      const int64_t cu = b * p.us0 + (d0 + vc) * p.us1 + (t0 + vt) * p.us2;
-      const int64_t cd = b * p.ds0 + (d0 + vc) * p.ds1 + (t0 + vt) * p.ds2;
-      const int64_t cz = b * p.zs0 + (d0 + vc) * p.zs1 + (t0 + vt) * p.zs2;
-      V8 zero = {};
-      ru = in ? *reinterpret_cast<const V8*>(static_cast<const T*>(u_) + cu) : zero;
-      rd = in ? *reinterpret_cast<const V8*>(static_cast<const T*>(delta_) + cd) : zero;
-      rz = (in && has_z) ? *reinterpret_cast<const V8*>(static_cast<const T*>(z_) + cz) : zero;
-    } else {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        const int64_t d = d0 + ec(j), t = t0 + et(j);
-        const bool in = d < p.dim && t < p.seqlen;
-        ru[j] = in ? static_cast<const T*>(u_)[b * p.us0 + d * p.us1 + t * p.us2] : T(0);
-        rd[j] = in ? static_cast<const T*>(delta_)[b * p.ds0 + d * p.ds1 + t * p.ds2] : T(0);
-        rz[j] = (in && has_z) ? static_cast<const T*>(z_)[b * p.zs0 + d * p.zs1 + t * p.zs2] : T(0);
-      }
-    }
-  };
-
-  const float* bcw = bc_ + (b * kGroups + g) * p.Lp * (2 * SPL);  // wave-uniform
-
-  if (p.ntiles > 0) load_raw(0);
-
-  for (int64_t tile = 0; tile < p.ntiles; ++tile) {
-    const int64_t t0 = tile * kT;
-
-    // ---- prologue: delta', delta'*u -> LDS; D*u and SiLU(z) stay in registers ----
-    float yskip[kVec], gate[kVec], dtv[kVec], duv[kVec];
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      const bool in = (d0 + ec(j) < p.dim) && (t0 + et(j) < p.seqlen);
-      const float uu = Ty<DT>::f(ru[j]);
-      const float dr = Ty<DT>::f(rd[j]);
-      const float dt = p.softplus ? softplus_cut(dr) : dr;
-      dtv[j] = in ? dt : 0.0f;  // identity step (a = 1, b = 0) outside the tensor
-      duv[j] = in ? dt * uu : 0.0f;
-      yskip[j] = Dv[j] * uu;
-      gate[j] = has_z ? silu_f(Ty<DT>::f(rz[j])) : 1.0f;
-    }
-    if (LAYOUT == kTimeContig) {
-      float4* pdt = reinterpret_cast<float4*>(&s_dt[vc][vt]);
-      float4* pdu = reinterpret_cast<float4*>(&s_du[vc][vt]);
-      pdt[0] = make_float4(dtv[0], dtv[1], dtv[2], dtv[3]);
-      pdt[1] = make_float4(dtv[4], dtv[5], dtv[6], dtv[7]);
-      pdu[0] = make_float4(duv[0], duv[1], duv[2], duv[3]);
-      pdu[1] = make_float4(duv[4], duv[5], duv[6], duv[7]);
-    } else {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        s_dt[vc + j][vt] = dtv[j];
-        s_du[vc + j][vt] = duv[j];
-      }
-    }
-    if (tile + 1 < p.ntiles) load_raw(t0 + kT);  // in flight during the scan
+  for (;;) {
+    // ---- claim a unit (segment-major tickets) ----
+    if (tid == 0) s_ticket = atomicAdd(&ctl_[0], 1);
     __syncthreads();
-
-    // ---- scan: lane = channel, wave = state group; B/C are SGPR operands ----
-    const float* q = bcw + t0 * (2 * SPL);
-#pragma unroll 2
-    for (int tt = 0; tt < kT; tt += 4) {
-      const float4 d4 = *reinterpret_cast<const float4*>(&s_dt[lane][tt]);
-      const float4 u4 = *reinterpret_cast<const float4*>(&s_du[lane][tt]);
-      const float dts[4] = {d4.x, d4.y, d4.z, d4.w};
-      const float dus[4] = {u4.x, u4.y, u4.z, u4.w};
-      float ys[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float* qq = q + (tt + j) * (2 * SPL);
-        float acc = 0.0f;
-#pragma unroll
-        for (int k = 0; k < SPL; ++k) {
-          const float a = exp2_hw(dts[j] * A2[k]);
-          h[k] = __builtin_fmaf(a, h[k], dus[j] * qq[k]);
-          acc = __builtin_fmaf(h[k], qq[SPL + k], acc);
-        }
-        ys[j] = acc;
-      }
-      *reinterpret_cast<float4*>(&s_y[g][lane][tt]) = make_float4(ys[0], ys[1], ys[2], ys[3]);
-    }
+    const int64_t unit = s_ticket;
     __syncthreads();
+    if (unit >= p.nunits) break;
+    const int64_t cb = unit % p.ncb;
+    const int64_t seg = unit / p.ncb;
+    const int64_t b = cb / p.nblk_d;
+    const int64_t d0 = (cb % p.nblk_d) * kCPW;
+    const int64_t tile0 = seg * p.seg_tiles;
+    const int64_t tile1 = std::min<int64_t>(tile0 + p.seg_tiles, p.Lp / kT);
 
-    // ---- epilogue: y = (sum_g partial + D*u) * SiLU(z) -> HBM ----
-    float yv[kVec];
-    if (LAYOUT == kTimeContig) {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) yv[j] = yskip[j];
-#pragma unroll
-      for (int gg = 0; gg < kGroups; ++gg) {
-        const float4* py = reinterpret_cast<const float4*>(&s_y[gg][vc][vt]);
-        const float4 a0 = py[0], a1 = py[1];
-        yv[0] += a0.x; yv[1] += a0.y; yv[2] += a0.z; yv[3] += a0.w;
-        yv[4] += a1.x; yv[5] += a1.y; yv[6] += a1.z; yv[7] += a1.w;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        float s = yskip[j];
-#pragma unroll
-        for (int gg = 0; gg < kGroups; ++gg) s += s_y[gg][vc + j][vt];
-        yv[j] = s;
-      }
-    }
-    V8 ry;
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) ry[j] = Ty<DT>::from(yv[j] * gate[j]);
-    if (p.vec_ok) {
-      if ((d0 + vc < p.dim) && (t0 + vt < p.seqlen))
-        *reinterpret_cast<V8*>(static_cast<T*>(y_) + b * p.ys0 + (d0 + vc) * p.ys1 +
-                               (t0 + vt) * p.ys2) = ry;
-    } else {
-#pragma unroll
-      for (int j = 0; j < kVec; ++j) {
-        const int64_t d = d0 + ec(j), t = t0 + et(j);
-        if (d < p.dim && t < p.seqlen) static_cast<T*>(y_)[b * p.ys0 + d * p.ys1 + t * p.ys2] = ry[j];
-      }
-    }
-  }
-
-  // ---- final state h[seqlen-1] (selective_scan_chunked.metal:151-155) ----
-  if (state_out_ != nullptr) {
-    const int64_t d = d0 + lane;
-    if (d < p.dim) {
+    // ---- per-lane constants ----
+    float Av[SPL], h[SPL];
+    {
+      const int64_t d = d0 + lane;
 #pragma unroll
       for (int k = 0; k < SPL; ++k) {
         const int64_t n = static_cast<int64_t>(g) * SPL + k;
-        if (n < p.dstate) state_out_[(b * p.dim + d) * p.dstate + n] = h[k];
+        Av[k] = (d < p.dim && n < p.dstate) ? p.A[d * p.As0 + n * p.As1] : 0.0f;
+        h[k] = 0.0f;
       }
     }
+    float Dv[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int64_t d = d0 + ec(j);
+      Dv[j] = (p.D != nullptr && d < p.dim) ? p.D[d * p.Ds] : 0.0f;
+    }
+
+    VE ru, rd, rz;
+    float4 rbc[BCPT];
+    auto load_raw = [&](int64_t t0) {
+#pragma unroll
+      for (int i = 0; i < BCPT; ++i) {
+        const int v = tid + i * NT;
+        if (v < BCV) {
+          const int gg = v / (kT * 2 * SPL / 4), rest = v % (kT * 2 * SPL / 4);
+          rbc[i] = *reinterpret_cast<const float4*>(
+              bc_ + ((b * G + gg) * p.Lp + t0) * (2 * SPL) + rest * 4);
+        }
+      }
+      if (p.vec_ok) {
+        const bool in = (d0 + vc < p.dim) && (t0 + vt < p.seqlen);
+        const int64_t cu = b * p.us0 + (d0 + vc) * p.us1 + (t0 + vt) * p.us2;
+        const int64_t cd = b * p.ds0 + (d0 + vc) * p.ds1 + (t0 + vt) * p.ds2;
+        const int64_t cz = b * p.zs0 + (d0 + vc) * p.zs1 + (t0 + vt) * p.zs2;
+        const VE zero = {};
+        ru = in ? *reinterpret_cast<const VE*>(static_cast<const T*>(u_) + cu) : zero;
+        rd = in ? *reinterpret_cast<const VE*>(static_cast<const T*>(delta_) + cd) : zero;
+        rz = (in && has_z) ? *reinterpret_cast<const VE*>(static_cast<const T*>(z_) + cz) : zero;
+      } else {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+          const int64_t d = d0 + ec(j), t = t0 + et(j);
+          const bool in = d < p.dim && t < p.seqlen;
+          ru[j] = in ? static_cast<const T*>(u_)[b * p.us0 + d * p.us1 + t * p.us2] : T(0);
+          rd[j] = in ? static_cast<const T*>(delta_)[b * p.ds0 + d * p.ds1 + t * p.ds2] : T(0);
+          rz[j] = (in && has_z) ? static_cast<const T*>(z_)[b * p.zs0 + d * p.zs1 + t * p.zs2]
+                                : T(0);
+        }
+      }
+    };
+
+    load_raw(tile0 * kT);
+
+    // ---- carried state from the previous segment of this chain ----
+    if (seg > 0) {
+      if (tid == 0) {
+        int spins = 0;
+        while (__hip_atomic_load(&ctl_[64 + cb], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+               static_cast<int>(seg)) {
+          __builtin_amdgcn_s_sleep(1);
+          if (++spins > kSpinLimit) {  // never expected; keeps every wave's exit bounded
+            __hip_atomic_store(&ctl_[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+        }
+      }
+      __syncthreads();
+      float* cp = carry_ + ((cb * G + g) * kCPW + lane) * SPL;
+#pragma unroll
+      for (int k = 0; k < SPL; ++k)
+        h[k] = __hip_atomic_load(cp + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    for (int64_t tile = tile0; tile < tile1; ++tile) {
+      const int64_t t0 = tile * kT;
+      const bool full = (t0 + kT <= p.seqlen) && (d0 + kCPW <= p.dim);
+
+      // ---- prologue ----
+      float yskip[EPT], gate[EPT], dtv[EPT], duv[EPT];
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        const float uu = Ty<DT>::f(ru[j]);
+        const float dr = Ty<DT>::f(rd[j]);
+        const float d2 = p.softplus ? softplus_log2<DT>(dr) : dr * kLog2e;
+        dtv[j] = d2;
+        duv[j] = d2 * uu;
+        yskip[j] = Dv[j] * uu;
+        gate[j] = has_z ? silu_f(Ty<DT>::f(rz[j])) : 1.0f;
+      }
+      if (!full) {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+          const bool in = (d0 + ec(j) < p.dim) && (t0 + et(j) < p.seqlen);
+          dtv[j] = in ? dtv[j] : 0.0f;  // identity step outside the tensor
+          duv[j] = in ? duv[j] : 0.0f;
+        }
+      }
+      if (LAYOUT == kTimeContig) {
+#pragma unroll
+        for (int j = 0; j < EPT; j += 4) {
+          *reinterpret_cast<float4*>(&s_dt[vc][vt + j]) = make_float4(dtv[j], dtv[j + 1], dtv[j + 2], dtv[j + 3]);
+          *reinterpret_cast<float4*>(&s_du[vc][vt + j]) = make_float4(duv[j], duv[j + 1], duv[j + 2], duv[j + 3]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+          s_dt[vc + j][vt] = dtv[j];
+          s_du[vc + j][vt] = duv[j];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < BCPT; ++i) {
+        const int v = tid + i * NT;
+        if (v < BCV) reinterpret_cast<float4*>(&s_bc[0][0][0])[v] = rbc[i];
+      }
+      if (tile + 1 < tile1) load_raw(t0 + kT);  // in flight during the scan
+      __syncthreads();
+
+      // ---- scan: lane = channel, wave = state group; LDS reads one group ahead ----
+      struct Grp {
+        float4 d4, u4;
+        float bc[4][2 * SPL];
+      };
+      auto fetch = [&](int tt, Grp& gr) {
+        gr.d4 = *reinterpret_cast<const float4*>(&s_dt[lane][tt]);
+        gr.u4 = *reinterpret_cast<const float4*>(&s_du[lane][tt]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int k = 0; k < 2 * SPL; ++k) gr.bc[j][k] = s_bc[g][tt + j][k];
+      };
+      Grp cur, nxt;
+      constexpr bool kPipe = SPL <= 4;
+      if (kPipe) fetch(0, nxt);
+#pragma unroll(kPipe ? 8 : 1)
+      for (int tt = 0; tt < kT; tt += 4) {
+        if (kPipe) {
+          cur = nxt;
+          if (tt + 4 < kT) fetch(tt + 4, nxt);
+        } else {
+          fetch(tt, cur);
+        }
+        const float dts[4] = {cur.d4.x, cur.d4.y, cur.d4.z, cur.d4.w};
+        const float dus[4] = {cur.u4.x, cur.u4.y, cur.u4.z, cur.u4.w};
+        float ys[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int k = 0; k < SPL; ++k) {
+            const float a = exp2_hw(dts[j] * Av[k]);
+            h[k] = __builtin_fmaf(a, h[k], dus[j] * cur.bc[j][k]);
+            acc = __builtin_fmaf(h[k], cur.bc[j][SPL + k], acc);
+          }
+          ys[j] = acc;
+        }
+        *reinterpret_cast<float4*>(&s_y[g][lane][tt]) = make_float4(ys[0], ys[1], ys[2], ys[3]);
+      }
+      __syncthreads();
+
+      // ---- epilogue: y = (sum_g partial + D*u) * SiLU(z) -> HBM ----
+      float yv[EPT];
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) yv[j] = yskip[j];
+      if (LAYOUT == kTimeContig) {
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+          for (int j = 0; j < EPT; j += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(&s_y[gg][vc][vt + j]);
+            yv[j] += a.x; yv[j + 1] += a.y; yv[j + 2] += a.z; yv[j + 3] += a.w;
+          }
+      } else {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+#pragma unroll
+          for (int gg = 0; gg < G; ++gg) yv[j] += s_y[gg][vc + j][vt];
+      }
+      VE ry;
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) ry[j] = Ty<DT>::from(yv[j] * gate[j]);
+      if (p.vec_ok) {
+        if ((d0 + vc < p.dim) && (t0 + vt < p.seqlen))
+          *reinterpret_cast<VE*>(static_cast<T*>(y_) + b * p.ys0 + (d0 + vc) * p.ys1 +
+                                 (t0 + vt) * p.ys2) = ry;
+      } else {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+          const int64_t d = d0 + ec(j), t = t0 + et(j);
+          if (d < p.dim && t < p.seqlen)
+            static_cast<T*>(y_)[b * p.ys0 + d * p.ys1 + t * p.ys2] = ry[j];
+        }
+      }
+    }
+
+    // ---- hand the state on, or write the final state ----
+    if (seg + 1 < p.nseg) {
+      float* cp = carry_ + ((cb * G + g) * kCPW + lane) * SPL;
+#pragma unroll
+      for (int k = 0; k < SPL; ++k)
+        __hip_atomic_store(cp + k, h[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // carry stores complete
+      __syncthreads();
+      if (tid == 0)
+        __hip_atomic_store(&ctl_[64 + cb], static_cast<int>(seg + 1), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    } else if (state_out_ != nullptr) {
+      const int64_t d = d0 + lane;
+      if (d < p.dim) {
+#pragma unroll
+        for (int k = 0; k < SPL; ++k) {
+          const int64_t n = static_cast<int64_t>(g) * SPL + k;
+          if (n < p.dstate) state_out_[(b * p.dim + d) * p.dstate + n] = h[k];
+        }
+      }
+    }
+    __syncthreads();  // LDS reuse by the next unit
   }
 }
 
 // ---------------------------------------------------------------------------
-template <int DT, int LAYOUT, int SPL>
-void launch(const Params& p, int64_t batch, hipStream_t s) {
-  dim3 grid(static_cast<unsigned>(ceil_div(p.dim, kCPW)), static_cast<unsigned>(batch));
-  hipLaunchKernelGGL((scan_kernel<DT, LAYOUT, SPL>), grid, dim3(kThreads), 0, s, p, p.u, p.delta,
-                     p.z, p.y, p.bc, p.state_out);
+// Workgroups per CU each instantiation can keep resident, per device (cached).
+template <typename K>
+int resident_per_cu(K kernel, int threads) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n < 1)
+    n = 1;
+  return n;
+}
+
+int num_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <int DT, int LAYOUT, int SPL, int G>
+void launch(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w) {
+  auto kern = scan_kernel<DT, LAYOUT, SPL, G>;
+  char* ws = static_cast<char*>(a->workspace);
+  int* ctl = reinterpret_cast<int*>(ws);
+  float* carry = reinterpret_cast<float*>(ws + w.carry);
+  const float* bc = reinterpret_cast<const float*>(ws + w.bc);
+  static int per_cu = 0;
+  if (per_cu == 0) per_cu = resident_per_cu(kern, kCPW * G);
+  const int64_t grid = std::min<int64_t>(p.nunits, static_cast<int64_t>(num_cus()) * per_cu);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(kCPW * G), 0, s, p, a->u,
+                     a->delta, a->z, a->y, bc, a->state_out, ctl, carry);
 }
 
 template <int DT, int LAYOUT>
-void launch_spl(const Params& p, int64_t batch, int spl, hipStream_t s) {
-  switch (spl) {
-    case 1: launch<DT, LAYOUT, 1>(p, batch, s); break;
-    case 2: launch<DT, LAYOUT, 2>(p, batch, s); break;
-    case 4: launch<DT, LAYOUT, 4>(p, batch, s); break;
-    case 8: launch<DT, LAYOUT, 8>(p, batch, s); break;
-    default: launch<DT, LAYOUT, 16>(p, batch, s); break;
-  }
+void launch_shape(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w, int groups,
+                  int spl) {
+  if (groups == 8 && spl == 1) launch<DT, LAYOUT, 1, 8>(p, a, s, w);
+  else if (groups == 8) launch<DT, LAYOUT, 2, 8>(p, a, s, w);
+  else if (spl == 8) launch<DT, LAYOUT, 8, 4>(p, a, s, w);
+  else launch<DT, LAYOUT, 16, 4>(p, a, s, w);
 }
 
 template <int DT>
-void launch_layout(const Params& p, int64_t batch, int layout, int spl, hipStream_t s) {
+void launch_layout(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w,
+                   int layout, int groups, int spl) {
   if (layout == kTimeContig)
-    launch_spl<DT, kTimeContig>(p, batch, spl, s);
+    launch_shape<DT, kTimeContig>(p, a, s, w, groups, spl);
   else
-    launch_spl<DT, kChanContig>(p, batch, spl, s);
+    launch_shape<DT, kChanContig>(p, a, s, w, groups, spl);
 }
 
 template <int DT>
-void launch_pack(const mm_scan_params* a, int64_t Lp, int spl, hipStream_t s) {
-  const int64_t total = a->batch * kGroups * spl * Lp;
+void launch_pack(const mm_scan_params* a, int64_t Lp, int groups, int spl, const WsLayout& w,
+                 int64_t nctl, hipStream_t s) {
+  const int64_t total = std::max<int64_t>(a->batch * groups * spl * Lp, nctl);
   const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 65536);
-  float* bc = static_cast<float*>(a->workspace);
-#define MM_PACK(S)                                                                         \
-  hipLaunchKernelGGL((pack_bc_kernel<DT, S>), dim3(static_cast<unsigned>(blocks)), dim3(256), \
-                     0, s, a->B, a->C, bc, a->batch, a->dstate, a->seqlen, Lp, a->B_stride[0], \
-                     a->B_stride[1], a->B_stride[2], a->C_stride[0], a->C_stride[1],        \
-                     a->C_stride[2])
-  switch (spl) {
-    case 1: MM_PACK(1); break;
-    case 2: MM_PACK(2); break;
-    case 4: MM_PACK(4); break;
-    case 8: MM_PACK(8); break;
-    default: MM_PACK(16); break;
-  }
+  char* ws = static_cast<char*>(a->workspace);
+  int* ctl = reinterpret_cast<int*>(ws);
+  float* bc = reinterpret_cast<float*>(ws + w.bc);
+#define MM_PACK(S, GG)                                                                          \
+  hipLaunchKernelGGL((pack_bc_kernel<DT, S, GG>), dim3(static_cast<unsigned>(blocks)), dim3(256), \
+                     0, s, a->B, a->C, bc, ctl, nctl, a->batch, a->dstate, a->seqlen, Lp,        \
+                     a->B_stride[0], a->B_stride[1], a->B_stride[2], a->C_stride[0],             \
+                     a->C_stride[1], a->C_stride[2])
+  if (groups == 8 && spl == 1) MM_PACK(1, 8);
+  else if (groups == 8) MM_PACK(2, 8);
+  else if (spl == 8) MM_PACK(8, 4);
+  else MM_PACK(16, 4);
 #undef MM_PACK
 }
 
@@ -324,7 +491,7 @@ struct Tens {
   const int64_t* s;
 };
 
-int choose_layout(const mm_scan_params* a, int* layout, int* vec_ok) {
+void choose_layout(const mm_scan_params* a, int ept, int* layout, int* vec_ok) {
   Tens ts[4] = {{a->u, a->u_stride}, {a->delta, a->delta_stride}, {a->y, a->y_stride},
                 {a->z, a->z_stride}};
   const int nt = a->z ? 4 : 3;
@@ -333,24 +500,16 @@ int choose_layout(const mm_scan_params* a, int* layout, int* vec_ok) {
     time_c = time_c && ts[i].s[2] == 1;
     chan_c = chan_c && ts[i].s[1] == 1;
   }
-  // Prefer the reference's own layout (time contiguous) when both hold (dim == 1 etc.).
   *layout = time_c ? kTimeContig : chan_c ? kChanContig : kTimeContig;
   bool ok = time_c || chan_c;
-  const int64_t es = dtype_size(a->x_dtype);
-  const int64_t vbytes = kVec * es;
-  if (ok) {
-    if (*layout == kTimeContig)
-      ok = a->seqlen % kVec == 0;
-    else
-      ok = a->dim % kVec == 0;
-  }
+  const int64_t vbytes = ept * dtype_size(a->x_dtype);
+  if (ok) ok = (*layout == kTimeContig) ? a->seqlen % ept == 0 : a->dim % ept == 0;
   for (int i = 0; ok && i < nt; ++i) {
     ok = aligned(ts[i].p, vbytes);
     const int64_t other = (*layout == kTimeContig) ? ts[i].s[1] : ts[i].s[2];
-    ok = ok && (other % kVec == 0) && (ts[i].s[0] % kVec == 0);
+    ok = ok && (other % ept == 0) && (ts[i].s[0] % ept == 0);
   }
   *vec_ok = ok ? 1 : 0;
-  return MM_OK;
 }
 
 int validate(const mm_scan_params* a) {
@@ -365,13 +524,8 @@ int validate(const mm_scan_params* a) {
   if (!valid_dtype(a->x_dtype) || !valid_dtype(a->bc_dtype))
     return fail(MM_ERR_DTYPE, "bad dtype (x_dtype=%d bc_dtype=%d)", a->x_dtype, a->bc_dtype);
   if (a->reserved != 0) return fail(MM_ERR_LAYOUT, "reserved field must be 0");
-  if (a->batch > 65535) return fail(MM_ERR_SHAPE, "batch=%lld exceeds 65535", (long long)a->batch);
-  const size_t need = mm_selective_scan_workspace_size(a->batch, a->dstate, a->seqlen);
-  if (need > 0 && (a->workspace == nullptr || a->workspace_bytes < need))
-    return fail(MM_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu (%s)", need,
-                a->workspace_bytes, a->workspace ? "too small" : "NULL");
-  if (a->workspace && !aligned(a->workspace, 16))
-    return fail(MM_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+  const int64_t ncb = a->batch * ceil_div(a->dim, kCPW);
+  if (ncb > (1LL << 30)) return fail(MM_ERR_SHAPE, "too many channel blocks (%lld)", (long long)ncb);
   return MM_OK;
 }
 
@@ -380,11 +534,13 @@ int validate(const mm_scan_params* a) {
 
 extern "C" {
 
-size_t mm_selective_scan_workspace_size(int64_t batch, int64_t dstate, int64_t seqlen) {
+size_t mm_selective_scan_workspace_size(int64_t batch, int64_t dim, int64_t dstate,
+                                        int64_t seqlen) {
   using namespace mm::scan;
-  if (batch <= 0 || seqlen <= 0 || dstate < 1 || dstate > MM_MAX_DSTATE) return 0;
-  const int64_t spl = spl_for(dstate);
-  return static_cast<size_t>(batch * kGroups * mm::round_up(seqlen, kT) * 2 * spl) * sizeof(float);
+  if (batch <= 0 || dim <= 0 || dstate < 1 || dstate > MM_MAX_DSTATE || seqlen < 0) return 0;
+  int groups = 8, spl = 2;
+  pick_shape(dstate, &groups, &spl);
+  return ws_layout(batch, dim, groups, spl, std::max<int64_t>(seqlen, 1)).total;
 }
 
 int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
@@ -395,24 +551,33 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
   if (st != MM_OK) return st;
   if (a->batch == 0 || a->dim == 0) return MM_OK;
 
+  int groups = 8, spl = 2;
+  pick_shape(a->dstate, &groups, &spl);
+  const int ept = kCPW * kT / (kCPW * groups);
   int layout = kTimeContig, vec_ok = 0;
-  choose_layout(a, &layout, &vec_ok);
-  const int spl = spl_for(a->dstate);
+  choose_layout(a, ept, &layout, &vec_ok);
+  const WsLayout w = ws_layout(a->batch, a->dim, groups, spl, std::max<int64_t>(a->seqlen, 1));
+  if (a->workspace == nullptr || a->workspace_bytes < w.total)
+    return fail(MM_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu (%s)", w.total,
+                a->workspace_bytes, a->workspace ? "too small" : "NULL");
+  if (!aligned(a->workspace, 256)) return fail(MM_ERR_WORKSPACE, "workspace must be 256-byte aligned");
 
   Params p;
-  p.u = a->u;
-  p.delta = a->delta;
-  p.z = a->z;
-  p.y = a->y;
   p.A = a->A;
   p.D = a->D;
-  p.state_out = a->state_out;
-  p.bc = static_cast<const float*>(a->workspace);
   p.dim = a->dim;
   p.dstate = a->dstate;
   p.seqlen = a->seqlen;
-  p.Lp = round_up(a->seqlen, kT);
-  p.ntiles = p.Lp / kT;
+  p.Lp = round_up(std::max<int64_t>(a->seqlen, 1), kT);
+  p.nblk_d = ceil_div(a->dim, kCPW);
+  p.ncb = a->batch * p.nblk_d;
+  const int64_t ntiles = p.Lp / kT;
+  // Segments: enough units that ~16 rounds keep every CU busy; at least 16 tiles each.
+  const int64_t target_units = static_cast<int64_t>(num_cus()) * 16;
+  int64_t nseg = std::max<int64_t>(1, std::min<int64_t>(ceil_div(target_units, p.ncb), ntiles / 16));
+  p.seg_tiles = ceil_div(ntiles, nseg);
+  p.nseg = ceil_div(ntiles, p.seg_tiles);
+  p.nunits = p.ncb * p.nseg;
   p.us0 = a->u_stride[0]; p.us1 = a->u_stride[1]; p.us2 = a->u_stride[2];
   p.ds0 = a->delta_stride[0]; p.ds1 = a->delta_stride[1]; p.ds2 = a->delta_stride[2];
   if (a->z) {
@@ -428,19 +593,18 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
   p.vec_ok = vec_ok;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (a->seqlen > 0) {
-    switch (a->bc_dtype) {
-      case MM_F32: launch_pack<MM_F32>(a, p.Lp, spl, s); break;
-      case MM_F16: launch_pack<MM_F16>(a, p.Lp, spl, s); break;
-      default: launch_pack<MM_BF16>(a, p.Lp, spl, s); break;
-    }
-    st = check_launch("pack_bc");
-    if (st != MM_OK) return st;
+  const int64_t nctl = 64 + p.ncb;
+  switch (a->bc_dtype) {
+    case MM_F32: launch_pack<MM_F32>(a, p.Lp, groups, spl, w, nctl, s); break;
+    case MM_F16: launch_pack<MM_F16>(a, p.Lp, groups, spl, w, nctl, s); break;
+    default: launch_pack<MM_BF16>(a, p.Lp, groups, spl, w, nctl, s); break;
   }
+  st = check_launch("pack_bc");
+  if (st != MM_OK) return st;
   switch (a->x_dtype) {
-    case MM_F32: launch_layout<MM_F32>(p, a->batch, layout, spl, s); break;
-    case MM_F16: launch_layout<MM_F16>(p, a->batch, layout, spl, s); break;
-    default: launch_layout<MM_BF16>(p, a->batch, layout, spl, s); break;
+    case MM_F32: launch_layout<MM_F32>(p, a, s, w, layout, groups, spl); break;
+    case MM_F16: launch_layout<MM_F16>(p, a, s, w, layout, groups, spl); break;
+    default: launch_layout<MM_BF16>(p, a, s, w, layout, groups, spl); break;
   }
   return check_launch("selective_scan");
 }

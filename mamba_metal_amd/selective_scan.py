@@ -63,7 +63,7 @@ def selective_scan_into(u, delta, A, B, C, y, *, D=None, z=None, delta_softplus=
         assert state_out.shape == (batch, dim, dstate) and state_out.is_contiguous()
         assert state_out.dtype == torch.float32
 
-    ws_bytes = lib.mm_selective_scan_workspace_size(batch, dstate, seqlen)
+    ws_bytes = lib.mm_selective_scan_workspace_size(batch, dim, dstate, seqlen)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
 
     p = _lib.ScanParams()

@@ -93,11 +93,11 @@ def _scan(lib, **over):
     (dict(dstate=0), _lib.ERR_DSTATE),
     (dict(batch=-1), _lib.ERR_SHAPE),
     (dict(seqlen=-5), _lib.ERR_SHAPE),
-    (dict(batch=70000), _lib.ERR_SHAPE),
     (dict(x_dtype=7), _lib.ERR_DTYPE),
     (dict(bc_dtype=-1), _lib.ERR_DTYPE),
     (dict(ws=None), _lib.ERR_WORKSPACE),
     (dict(ws_bytes=16), _lib.ERR_WORKSPACE),
+    (dict(ws=FAKE + 16), _lib.ERR_WORKSPACE),
 ])
 def test_scan_validation_errors(lib, over, status):
     st = _scan(lib, **over)
@@ -107,12 +107,17 @@ def test_scan_validation_errors(lib, over, status):
 
 
 def test_workspace_size(lib):
-    # batch * 4 groups * round_up(seqlen, 32) * 2 * states-per-lane floats
-    assert lib.mm_selective_scan_workspace_size(4, 16, 32768) == 4 * 4 * 32768 * 2 * 4 * 4
-    assert lib.mm_selective_scan_workspace_size(1, 16, 1) == 1 * 4 * 32 * 8 * 4
-    assert lib.mm_selective_scan_workspace_size(1, 64, 100) == 4 * 128 * 32 * 4
-    assert lib.mm_selective_scan_workspace_size(1, 65, 100) == 0
-    assert lib.mm_selective_scan_workspace_size(0, 16, 100) == 0
+    # control block (256 B) + flags + carried state + packed fp32 B/C (16 states -> 8
+    # groups x 2 per lane, padded to 32-step tiles)
+    ncb = 4 * 5120 // 64
+    flags_end = 256 + 4 * ncb
+    carry = -(-flags_end // 256) * 256
+    bc = -(-(carry + 4 * ncb * 16 * 64) // 256) * 256
+    assert lib.mm_selective_scan_workspace_size(4, 5120, 16, 32768) == bc + 4 * 4 * 16 * 32768 * 2
+    assert lib.mm_selective_scan_workspace_size(1, 64, 65, 100) == 0
+    assert lib.mm_selective_scan_workspace_size(0, 64, 16, 100) == 0
+    assert lib.mm_selective_scan_workspace_size(1, 64, 64, 100) > \
+        lib.mm_selective_scan_workspace_size(1, 64, 16, 100)
 
 
 def test_strided_null_params(lib):
