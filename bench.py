@@ -203,6 +203,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--copy-probe-only", action="store_true",
+                    help="run only the 2 GiB device copy (HBM counter calibration)")
     ap.add_argument("--only-scan", action="store_true",
                     help="config-4 scan only (the command the committed rocprof summaries use)")
     args = ap.parse_args()
@@ -217,6 +219,9 @@ def main():
 
     from mamba_metal_amd import _lib
 
+    if args.copy_probe_only:
+        print(json.dumps({"copy_probe_gbs": copy_probe_gbs(), "bytes_per_copy": 2 * (1 << 30)}))
+        return
     _lib.load()
     torch.backends.cuda.matmul.allow_tf32 = False
     B, D, N, L = 4, 5120, 16, 32768
