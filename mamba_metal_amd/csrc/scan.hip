@@ -391,7 +391,11 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
 #pragma unroll
       for (int k = 0; k < SPL; ++k)
         __hip_atomic_store(cp + k, h[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // carry stores complete
+      // Release without an L2 writeback: the carry stores are device-coherent (sc1), so
+      // waiting for them to complete (vmcnt(0)) in every wave before the barrier orders
+      // them before the flag store below.  A workgroup-scope fence would not wait for
+      // global stores, and an agent-scope one would write back the whole L2.
+      __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (tid == 0)
         __hip_atomic_store(&ctl_[64 + cb], static_cast<int>(seg + 1), __ATOMIC_RELAXED,
