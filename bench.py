@@ -205,6 +205,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--copy-probe-only", action="store_true",
                     help="run only the 2 GiB device copy (HBM counter calibration)")
+    ap.add_argument("--only-decode", choices=["130m", "2.8b"],
+                    help="run one decode benchmark only (the command of the decode profiles)")
     ap.add_argument("--only-scan", action="store_true",
                     help="config-4 scan only (the command the committed rocprof summaries use)")
     args = ap.parse_args()
@@ -219,6 +221,16 @@ def main():
 
     from mamba_metal_amd import _lib
 
+    if args.only_decode:
+        _lib.load()
+        if args.only_decode == "130m":
+            r = decode_bench("130m", dict(d_model=768, n_layer=24, vocab_size=50280, dt_rank=48),
+                             1, 2048, 128)
+        else:
+            r = decode_bench("2.8b", dict(d_model=2560, n_layer=64, vocab_size=50280, dt_rank=160),
+                             64, 512, 256)
+        print(json.dumps(r))
+        return
     if args.copy_probe_only:
         print(json.dumps({"copy_probe_gbs": copy_probe_gbs(), "bytes_per_copy": 2 * (1 << 30)}))
         return

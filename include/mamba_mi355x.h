@@ -173,6 +173,83 @@ int mm_decode_ssm_step(float* ssm_state, const void* x, const void* dt, const fl
                        int64_t C_stride_b, int64_t z_stride_b, int64_t y_stride_b,
                        int32_t x_dtype, int32_t dt_softplus, void* stream);
 
+/* Fused SSM step with the dt projection folded in -- replaces mamba_block.py:183-195
+ * together with the dt_proj Linear of :183:
+ *   dt[b,c] = softplus(dt_bias[c] + sum_r dt_in[b,r] * dt_weight[c,r])
+ * then the update of mm_decode_ssm_step.  dt_in (batch, rank) with batch stride
+ * dt_stride_b and unit stride (the dt slice of x_proj's output); dt_weight (dim, rank)
+ * with row stride w_stride_c, dt_bias (dim,) in w_dtype (may be NULL); rank <= 256.
+ * Other arguments as mm_decode_ssm_step. */
+int mm_decode_ssm_step_dtproj(float* ssm_state, const void* x, const void* dt_in,
+                              const void* dt_weight, const void* dt_bias, const float* A,
+                              const void* B, const void* C, const float* D, const void* z,
+                              void* y, int64_t batch, int64_t dim, int64_t dstate, int64_t rank,
+                              int64_t x_stride_b, int64_t dt_stride_b, int64_t w_stride_c,
+                              int64_t B_stride_b, int64_t C_stride_b, int64_t z_stride_b,
+                              int64_t y_stride_b, int32_t x_dtype, int32_t w_dtype, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Fused residual add + RMSNorm -- replaces `x + mixer(...)` followed by the next
+ * layer's nn.RMSNorm (mamba_model.py:40,48,53,57,69):
+ *   resid[r,:] += add[r,:]           (skipped when add is NULL; kept in x_dtype)
+ *   out[r,:]    = resid[r,:] * rsqrt(mean(resid[r,:]^2) + eps) * weight
+ * rows x dim, row strides given, unit column stride; weight (dim,) in w_dtype;
+ * dim <= 8192. */
+int mm_add_rmsnorm(void* resid, const void* add, const void* weight, void* out, int64_t rows,
+                   int64_t dim, int64_t resid_stride, int64_t add_stride, int64_t out_stride,
+                   float eps, int32_t x_dtype, int32_t w_dtype, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Decode-step GEMM with fused epilogues -- replaces the nn.Linear projections of
+ * MambaBlock.step (in_proj mamba_block.py:166, x_proj :180, out_proj :196) and the
+ * tied LM head (mamba_model.py:78) at decode batch M <= 64:
+ *   acc[m, n] = sum_k x[m, k] * w[n, k]          (w is nn.Linear's (N, K) weight)
+ * epilogue MM_LIN_STORE: y[m, n] = acc.
+ * epilogue MM_LIN_RESID: resid[m, n] = resid[m, n] + round(acc)  (out_proj followed
+ *   by the residual add of mamba_model.py:48; y unused).
+ * epilogue MM_LIN_CONV:  in_proj followed by the conv-window step of
+ *   mamba_block.py:172-179 on columns [0, n_conv): x = round(acc); conv_state
+ *   (M, n_conv, 4) contiguous shifts in place; conv_out[m, n] = silu(conv_b[n] +
+ *   sum_j conv_w[n, j] * window_j); columns >= n_conv store y[m, n - n_conv] = acc.
+ * w is passed PACKED (mm_pack_linear_weight, once per weight).  f16 / bf16 only
+ * (one dtype for every tensor); K a multiple of 64; ldx >= K a multiple of 8; x
+ * and w_packed 16-byte aligned.  Narrow N splits K across workgroups: fp32
+ * partials go to the workspace (mm_decode_linear_workspace_size bytes, 16-byte
+ * aligned, no initial contents needed) and a second kernel sums them; calls that
+ * overlap in time must not share a workspace. */
+typedef enum mm_linear_epilogue {
+  MM_LIN_STORE = 0,
+  MM_LIN_RESID = 1,
+  MM_LIN_CONV = 2
+} mm_linear_epilogue;
+
+typedef struct mm_linear_params {
+  const void* x;          /* (M, K), row stride ldx */
+  const void* w_packed;   /* mm_pack_linear_weight output for the (N, K) weight */
+  void* y;                /* (M, N) row stride ldy (CONV: (M, N - n_conv)) */
+  void* resid;            /* RESID: (M, N) row stride ldr */
+  void* conv_state;       /* CONV: (M, n_conv, 4) contiguous */
+  const void* conv_w;     /* CONV: (n_conv, 4) contiguous */
+  const void* conv_b;     /* CONV: (n_conv,) or NULL */
+  void* conv_out;         /* CONV: (M, n_conv) row stride ldc */
+  void* workspace;        /* split-K counters + partial tiles (may be NULL if size 0) */
+  size_t workspace_bytes;
+  int64_t M, N, K;
+  int64_t ldx, ldy, ldr, ldc;
+  int64_t n_conv;
+  int32_t dtype;          /* MM_F16 or MM_BF16 */
+  int32_t epilogue;       /* mm_linear_epilogue */
+} mm_linear_params;
+
+/* Bytes of the packed copy of an (N, K) weight: ceil(N/32)*32 * K elements. */
+size_t mm_packed_linear_weight_bytes(int64_t N, int64_t K, int32_t dtype);
+/* Repack w (N, K), row stride ldw, into the decode GEMM's operand order. */
+int mm_pack_linear_weight(const void* w, void* packed, int64_t N, int64_t K, int64_t ldw,
+                          int32_t dtype, void* stream);
+/* Workspace bytes mm_decode_linear needs for (M, N, K); 0 when it needs none. */
+size_t mm_decode_linear_workspace_size(int64_t M, int64_t N, int64_t K);
+int mm_decode_linear(const mm_linear_params* params, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Pair-scan primitive -- replaces mamba_metal/kernels/pair_scan.metal:1-76
  * (dispatched by experiments/05-pair-scan/pair_scan.py:23-33), without its

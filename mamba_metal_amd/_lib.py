@@ -59,6 +59,19 @@ class ScanParams(ctypes.Structure):
     ]
 
 
+class LinearParams(ctypes.Structure):
+    """Mirror of ``mm_linear_params`` (include/mamba_mi355x.h)."""
+
+    _fields_ = [
+        ("x", _vp), ("w_packed", _vp), ("y", _vp), ("resid", _vp), ("conv_state", _vp),
+        ("conv_w", _vp), ("conv_b", _vp), ("conv_out", _vp), ("workspace", _vp),
+        ("workspace_bytes", _sz),
+        ("M", _i64), ("N", _i64), ("K", _i64),
+        ("ldx", _i64), ("ldy", _i64), ("ldr", _i64), ("ldc", _i64),
+        ("n_conv", _i64), ("dtype", _i32), ("epilogue", _i32),
+    ]
+
+
 _SIGNATURES = {
     "mm_abi_version": ([], ctypes.c_int),
     "mm_last_error": ([], ctypes.c_char_p),
@@ -73,6 +86,13 @@ _SIGNATURES = {
         [_vp] * 5 + [_i64] * 5 + [_i64a2, _i32, _i32, _i32, _i32, _vp], ctypes.c_int),
     "mm_decode_ssm_step": (
         [_vp] * 10 + [_i64] * 9 + [_i32, _i32, _vp], ctypes.c_int),
+    "mm_decode_ssm_step_dtproj": (
+        [_vp] * 11 + [_i64] * 11 + [_i32, _i32, _vp], ctypes.c_int),
+    "mm_add_rmsnorm": ([_vp] * 4 + [_i64] * 5 + [ctypes.c_float, _i32, _i32, _vp], ctypes.c_int),
+    "mm_packed_linear_weight_bytes": ([_i64, _i64, _i32], _sz),
+    "mm_pack_linear_weight": ([_vp, _vp, _i64, _i64, _i64, _i32, _vp], ctypes.c_int),
+    "mm_decode_linear_workspace_size": ([_i64, _i64, _i64], _sz),
+    "mm_decode_linear": ([ctypes.POINTER(LinearParams), _vp], ctypes.c_int),
     "mm_pair_scan": ([_vp] * 4 + [_i64, _vp], ctypes.c_int),
 }
 

@@ -206,6 +206,35 @@ __global__ __launch_bounds__(kBlock) void conv_step_kernel(const StepParams p) {
   st_any(p.out, b * p.osb + c, p.apply_silu ? silu_f(acc) : acc, p.x_dtype);
 }
 
+// Fast decode step for the common layout: width 4, state, x and weight of one
+// dtype, state rows and weight rows contiguous and aligned.  The 4-tap window and
+// the weight row move as single 8/16-byte vectors; the shifted window is written
+// back with one vector store.
+template <int DT>
+__global__ __launch_bounds__(kBlock) void conv_step4_kernel(const StepParams p) {
+  using T = typename Ty<DT>::T;
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (c >= p.dim) return;
+  T4* sp = static_cast<T4*>(p.state) + b * p.dim + c;
+  const T4 win = *sp;
+  const T4 wv = static_cast<const T4*>(p.w)[c];
+  const T xr = static_cast<const T*>(p.x)[b * p.xsb + c];
+  float acc = p.bias ? ld<DT>(p.bias, c) : 0.0f;
+  acc = __builtin_fmaf(Ty<DT>::f(wv[0]), Ty<DT>::f(win[1]), acc);
+  acc = __builtin_fmaf(Ty<DT>::f(wv[1]), Ty<DT>::f(win[2]), acc);
+  acc = __builtin_fmaf(Ty<DT>::f(wv[2]), Ty<DT>::f(win[3]), acc);
+  acc = __builtin_fmaf(Ty<DT>::f(wv[3]), Ty<DT>::f(xr), acc);
+  T4 nw;
+  nw[0] = win[1];
+  nw[1] = win[2];
+  nw[2] = win[3];
+  nw[3] = xr;
+  *sp = nw;
+  st<DT>(p.out, b * p.osb + c, p.apply_silu ? silu_f(acc) : acc);
+}
+
 }  // namespace conv
 }  // namespace mm
 
@@ -302,7 +331,20 @@ int mm_decode_conv_step(void* conv_state, const void* x, const void* weight, con
   p.w_dtype = w_dtype;
   p.apply_silu = apply_silu ? 1 : 0;
   const dim3 grid(static_cast<unsigned>(ceil_div(dim, kBlock)), static_cast<unsigned>(batch));
-  hipLaunchKernelGGL(conv_step_kernel, grid, dim3(kBlock), 0, static_cast<hipStream_t>(stream), p);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t vb = 4 * dtype_size(x_dtype);
+  const bool fast = width == 4 && state_dtype == x_dtype && w_dtype == x_dtype &&
+                    w_stride[1] == 1 && w_stride[0] == 4 && aligned(conv_state, vb) &&
+                    aligned(weight, vb);
+  if (fast) {
+    switch (x_dtype) {
+      case MM_F32: hipLaunchKernelGGL((conv_step4_kernel<MM_F32>), grid, dim3(kBlock), 0, s, p); break;
+      case MM_F16: hipLaunchKernelGGL((conv_step4_kernel<MM_F16>), grid, dim3(kBlock), 0, s, p); break;
+      default: hipLaunchKernelGGL((conv_step4_kernel<MM_BF16>), grid, dim3(kBlock), 0, s, p); break;
+    }
+  } else {
+    hipLaunchKernelGGL(conv_step_kernel, grid, dim3(kBlock), 0, s, p);
+  }
   return check_launch("decode_conv_step");
 }
 

@@ -151,3 +151,283 @@ int mm_decode_ssm_step(float* ssm_state, const void* x, const void* dt, const fl
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Fused decode SSM step with the dt projection folded in: mm_decode_ssm_step_dtproj.
+//
+// Replaces mamba_block.py:183-195 INCLUDING the dt_proj Linear of :183:
+//   dt[b,c] = softplus(bias[c] + sum_r dt_in[b,r] * W[c,r])
+// followed by the state update of mm_decode_ssm_step (dstate == 16, the Mamba-1
+// checkpoints' value).
+//
+// Lane layout: a channel's 16-float state row is split over a quad of 4
+// consecutive lanes (4 states = one float4 each), so a wave covers 16 channels and
+// every state access of a wave is 1 KB contiguous.  The rank-R dot product is
+// split over the quad the same way: lane q holds W[c, q*RQ : (q+1)*RQ] in
+// registers -- loaded once, reused for every batch row of the workgroup -- and
+// reads the matching dt_in slice from LDS (padded so the quad's four broadcast
+// reads hit distinct banks); two quad shuffles finish the dot and the C
+// contraction.  All state rows of the workgroup are loaded before any compute so
+// the kernel keeps kBB x 16 bytes per lane in flight: it is HBM-bound on the
+// 2 x 64 bytes of state per (b, c).
+namespace mm {
+namespace dec {
+
+constexpr int kFusedWaves = 2;
+constexpr int kFusedCh = kFusedWaves * 16;   // channels per workgroup
+constexpr int kFusedBB = 8;                  // batch rows per workgroup
+constexpr int kFusedNS = 16;
+constexpr int kMaxRank = 256;
+
+struct FusedParams {
+  float* h;
+  const void* x;
+  const void* dt_in;
+  const void* w;
+  const void* bias;
+  const float* A;
+  const void* B;
+  const void* C;
+  const float* D;
+  const void* z;
+  void* y;
+  int64_t batch, dim, rank;
+  int64_t xsb, dtsb, wsc, Bsb, Csb, zsb, ysb;
+  int32_t wvec;  // W rows 16-byte aligned and rank % 8 == 0: 8-element vector loads
+};
+
+// 8 consecutive elements at p (16-byte aligned for 2-byte types, 32 for fp32).
+template <int DT>
+__device__ __forceinline__ void ld8(const void* p, float* out) {
+  using V8 = typename Ty<DT>::V8;
+  const V8 v = *static_cast<const V8*>(p);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) out[k] = Ty<DT>::f(v[k]);
+}
+
+template <int DT, int RQ, bool WVEC>
+__global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_dtproj_kernel(const FusedParams p) {
+  using T = typename Ty<DT>::T;
+  using V8 = typename Ty<DT>::V8;
+  constexpr int RQP = RQ + 4;  // padded slice stride: quad reads land in distinct banks
+  constexpr int NT = kFusedWaves * 64;
+  __shared__ float s_dt[kFusedBB][4 * RQP];
+  __shared__ float s_B[kFusedBB][kFusedNS];
+  __shared__ float s_C[kFusedBB][kFusedNS];
+  const int tid = threadIdx.x;
+  const int q = tid & 3;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * kFusedCh + (tid >> 2);
+  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * kFusedBB;
+  const int nb = static_cast<int>(p.batch - b0 < kFusedBB ? p.batch - b0 : kFusedBB);
+  const int R = static_cast<int>(p.rank);
+  const bool cok = c < p.dim;
+  // Every load below is unconditional from a clamped, in-bounds address (channel 0
+  // past dim, row b0 past the batch, index 0 past rank); the values are masked at
+  // their first use, so all loads are in flight together.
+  const int64_t cc = cok ? c : 0;
+  const T* const zp = static_cast<const T*>(p.z ? p.z : p.x);
+
+  float4 hv[kFusedBB];
+  T xr[kFusedBB], zr[kFusedBB];
+#pragma unroll
+  for (int bb = 0; bb < kFusedBB; ++bb) {
+    const int64_t b = b0 + (bb < nb ? bb : 0);
+    hv[bb] = *reinterpret_cast<const float4*>(p.h + (b * p.dim + cc) * kFusedNS + q * 4);
+    xr[bb] = static_cast<const T*>(p.x)[b * p.xsb + cc];
+    zr[bb] = zp[p.z ? b * p.zsb + cc : b * p.xsb + cc];
+  }
+  // This lane's slice of W[c, :] (zero beyond rank).
+  const int r0 = q * RQ;
+  float w[RQ];
+  if constexpr (WVEC) {
+    V8 raw[RQ / 8];
+#pragma unroll
+    for (int i = 0; i < RQ / 8; ++i) {
+      const int r = r0 + 8 * i < R ? r0 + 8 * i : 0;
+      raw[i] = *reinterpret_cast<const V8*>(static_cast<const T*>(p.w) + cc * p.wsc + r);
+    }
+#pragma unroll
+    for (int i = 0; i < RQ / 8; ++i)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) w[8 * i + k] = (r0 + 8 * i < R) ? Ty<DT>::f(raw[i][k]) : 0.0f;
+  } else {
+    T raw[RQ];
+#pragma unroll
+    for (int i = 0; i < RQ; ++i) {
+      const int r = r0 + i < R ? r0 + i : 0;
+      raw[i] = static_cast<const T*>(p.w)[cc * p.wsc + r];
+    }
+#pragma unroll
+    for (int i = 0; i < RQ; ++i) w[i] = (r0 + i < R) ? Ty<DT>::f(raw[i]) : 0.0f;
+  }
+  float4 Av = *reinterpret_cast<const float4*>(p.A + cc * kFusedNS + q * 4);
+  const T biasr = static_cast<const T*>(p.bias ? p.bias : p.x)[p.bias ? cc : 0];
+  const float Dr = p.D ? p.D[cc] : 0.0f;
+
+  // dt_in rows, B and C of the batch block -> LDS (zero past rank / batch).
+  constexpr int NDT = (kFusedBB * 4 * RQ + NT - 1) / NT;
+  T dtr[NDT];
+#pragma unroll
+  for (int u = 0; u < NDT; ++u) {
+    const int e = tid + u * NT;
+    const int bb = e / (4 * RQ), r = e % (4 * RQ);
+    const bool ok = e < kFusedBB * 4 * RQ && bb < nb && r < R;
+    dtr[u] = static_cast<const T*>(p.dt_in)[ok ? (b0 + bb) * p.dtsb + r : 0];
+  }
+  constexpr int NBC = (kFusedBB * kFusedNS + NT - 1) / NT;
+  T br[NBC], cr[NBC];
+#pragma unroll
+  for (int u = 0; u < NBC; ++u) {
+    const int e = tid + u * NT;
+    const int bb = e / kFusedNS, n = e % kFusedNS;
+    const bool ok = e < kFusedBB * kFusedNS && bb < nb;
+    br[u] = static_cast<const T*>(p.B)[ok ? (b0 + bb) * p.Bsb + n : 0];
+    cr[u] = static_cast<const T*>(p.C)[ok ? (b0 + bb) * p.Csb + n : 0];
+  }
+#pragma unroll
+  for (int u = 0; u < NDT; ++u) {
+    const int e = tid + u * NT;
+    const int bb = e / (4 * RQ), r = e % (4 * RQ);
+    if (e < kFusedBB * 4 * RQ)
+      s_dt[bb][(r / RQ) * RQP + r % RQ] = (bb < nb && r < R) ? Ty<DT>::f(dtr[u]) : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < NBC; ++u) {
+    const int e = tid + u * NT;
+    const int bb = e / kFusedNS, n = e % kFusedNS;
+    if (e < kFusedBB * kFusedNS) {
+      s_B[bb][n] = bb < nb ? Ty<DT>::f(br[u]) : 0.0f;
+      s_C[bb][n] = bb < nb ? Ty<DT>::f(cr[u]) : 0.0f;
+    }
+  }
+  __syncthreads();
+
+  const float Al[4] = {Av.x * kLog2e, Av.y * kLog2e, Av.z * kLog2e, Av.w * kLog2e};
+  const float bias = p.bias ? Ty<DT>::f(biasr) : 0.0f;
+  float* hw = p.h + (b0 * p.dim + cc) * kFusedNS + q * 4;
+#pragma unroll
+  for (int bb = 0; bb < kFusedBB; ++bb) {
+    if (bb >= nb) break;
+    const float4* sd = reinterpret_cast<const float4*>(&s_dt[bb][q * RQP]);
+    float dot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RQ / 4; ++i) {
+      const float4 d = sd[i];
+      dot = __builtin_fmaf(d.x, w[4 * i], dot);
+      dot = __builtin_fmaf(d.y, w[4 * i + 1], dot);
+      dot = __builtin_fmaf(d.z, w[4 * i + 2], dot);
+      dot = __builtin_fmaf(d.w, w[4 * i + 3], dot);
+    }
+    dot += __shfl_xor(dot, 1, 64);
+    dot += __shfl_xor(dot, 2, 64);
+    const float xv = Ty<DT>::f(xr[bb]);
+    const float dtv = softplus_full(dot + bias);
+    const float du = dtv * xv;
+    float hs[4] = {hv[bb].x, hv[bb].y, hv[bb].z, hv[bb].w};
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float a = exp2_hw(dtv * Al[k]);
+      hs[k] = __builtin_fmaf(a, hs[k], du * s_B[bb][q * 4 + k]);
+      acc = __builtin_fmaf(hs[k], s_C[bb][q * 4 + k], acc);
+    }
+    if (cok) *reinterpret_cast<float4*>(hw + bb * p.dim * kFusedNS) = make_float4(hs[0], hs[1], hs[2], hs[3]);
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    if (q == 0 && cok) {
+      acc = __builtin_fmaf(Dr, xv, acc);
+      if (p.z) acc *= silu_f(Ty<DT>::f(zr[bb]));
+      st<DT>(p.y, (b0 + bb) * p.ysb + c, acc);
+    }
+  }
+}
+
+template <int DT, bool WV>
+void launch_fused_w(const FusedParams& p, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(ceil_div(p.dim, kFusedCh)),
+                  static_cast<unsigned>(ceil_div(p.batch, kFusedBB)));
+  const dim3 block(kFusedWaves * 64);
+  const int64_t rq = ceil_div(p.rank, 4);
+  if (rq <= 16)
+    hipLaunchKernelGGL((ssm_step_dtproj_kernel<DT, 16, WV>), grid, block, 0, s, p);
+  else if (rq <= 32)
+    hipLaunchKernelGGL((ssm_step_dtproj_kernel<DT, 32, WV>), grid, block, 0, s, p);
+  else if (rq <= 48)
+    hipLaunchKernelGGL((ssm_step_dtproj_kernel<DT, 48, WV>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((ssm_step_dtproj_kernel<DT, 64, WV>), grid, block, 0, s, p);
+}
+
+template <int DT>
+void launch_fused(const FusedParams& p, hipStream_t s) {
+  if (p.wvec) launch_fused_w<DT, true>(p, s);
+  else launch_fused_w<DT, false>(p, s);
+}
+
+}  // namespace dec
+}  // namespace mm
+
+extern "C" {
+
+int mm_decode_ssm_step_dtproj(float* ssm_state, const void* x, const void* dt_in,
+                              const void* dt_weight, const void* dt_bias, const float* A,
+                              const void* B, const void* C, const float* D, const void* z,
+                              void* y, int64_t batch, int64_t dim, int64_t dstate, int64_t rank,
+                              int64_t x_stride_b, int64_t dt_stride_b, int64_t w_stride_c,
+                              int64_t B_stride_b, int64_t C_stride_b, int64_t z_stride_b,
+                              int64_t y_stride_b, int32_t x_dtype, int32_t w_dtype, void* stream) {
+  using namespace mm;
+  using namespace mm::dec;
+  clear_error();
+  if (!ssm_state || !x || !dt_in || !dt_weight || !A || !B || !C || !y)
+    return fail(MM_ERR_NULL_POINTER, "ssm_state, x, dt_in, dt_weight, A, B, C and y are required");
+  if (batch < 0 || dim < 0) return fail(MM_ERR_SHAPE, "negative size");
+  if (rank < 1 || rank > kMaxRank)
+    return fail(MM_ERR_SHAPE, "rank=%lld outside [1, %d]", (long long)rank, kMaxRank);
+  if (dstate != kFusedNS)
+    return fail(MM_ERR_DSTATE, "dstate=%lld: the fused step supports dstate == %d",
+                (long long)dstate, kFusedNS);
+  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype)) return fail(MM_ERR_DTYPE, "bad dtype");
+  if (w_dtype != x_dtype)
+    return fail(MM_ERR_DTYPE, "dt_weight dtype %d differs from x dtype %d", w_dtype, x_dtype);
+  if (!aligned(ssm_state, 16) || !aligned(A, 16))
+    return fail(MM_ERR_LAYOUT, "ssm_state and A must be 16-byte aligned");
+  if (ceil_div(batch, kFusedBB) > 65535) return fail(MM_ERR_SHAPE, "batch too large");
+  if (batch == 0 || dim == 0) return MM_OK;
+  FusedParams p;
+  p.h = ssm_state;
+  p.x = x;
+  p.dt_in = dt_in;
+  p.w = dt_weight;
+  p.bias = dt_bias;
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  p.D = D;
+  p.z = z;
+  p.y = y;
+  p.batch = batch;
+  p.dim = dim;
+  p.rank = rank;
+  p.xsb = x_stride_b;
+  p.dtsb = dt_stride_b;
+  p.wsc = w_stride_c;
+  p.Bsb = B_stride_b;
+  p.Csb = C_stride_b;
+  p.zsb = z_stride_b;
+  p.ysb = y_stride_b;
+  {
+    const int64_t vb = x_dtype == MM_F32 ? 32 : 16;  // bytes of 8 elements
+    const int64_t es = dtype_size(x_dtype);
+    p.wvec = (rank % 8 == 0) && aligned(dt_weight, vb) && ((w_stride_c * es) % vb == 0) ? 1 : 0;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (x_dtype) {
+    case MM_F32: launch_fused<MM_F32>(p, s); break;
+    case MM_F16: launch_fused<MM_F16>(p, s); break;
+    default: launch_fused<MM_BF16>(p, s); break;
+  }
+  return check_launch("decode_ssm_step_dtproj");
+}
+
+}  // extern "C"

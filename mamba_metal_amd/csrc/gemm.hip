@@ -1,0 +1,556 @@
+// Weight-streaming GEMM for the decode step: mm_decode_linear, mm_pack_linear_weight.
+//
+//   Y[M, N] = X[M, K] . W[N, K]^T          (M <= 64 rows: one token per sequence)
+//
+// covers the nn.Linear projections of MambaBlock.step (in_proj, x_proj, out_proj;
+// mamba_metal/mamba_block.py:166-196) and the tied LM head (mamba_model.py:78) at
+// decode batch M.  With M <= 64 each weight element is used M times and read once:
+// the kernel is HBM-bound on N*K*elem bytes of W.
+//
+// Packed weights.  W is repacked once (mm_pack_linear_weight) into the operand
+// order of v_mfma_f32_32x32x16: block (t, s) of 1 KB holds, for lane l, the 8
+// elements W[32t + l%32, 16s + 8(l/32) .. +7].  A wave's W load for one MFMA step
+// is then one 1 KB contiguous read -- the access pattern of a plain stream.
+//
+// X goes through LDS: each wave loads its 64-row x 64-k chunk of X with 128-byte
+// row segments (8 rows per load instruction), writes it to a wave-private LDS tile
+// (rows padded to 144 bytes) and reads its A operands from there.
+//
+// Work split.  A workgroup owns NT x 32 output columns (NT = 2 for wide N, so each
+// X operand feeds two MFMAs).  Wide calls keep all of K in the workgroup: its KSW
+// waves split K, their partial tiles meet in LDS (summed in fixed wave order) and
+// the epilogue runs in the same kernel.  Narrow calls (too few column tiles to fill
+// the chip) split K over the grid's y dimension instead: single-wave workgroups
+// write fp32 partial tiles, row-major [split][M][N], to the workspace, and a second
+// kernel sums the splits in order and runs the epilogue -- deterministic, and the
+// kernel boundary orders the partials without any cross-workgroup protocol.
+//
+// Epilogues fold the decode step's neighbouring element-wise ops into the GEMM:
+//   MM_LIN_STORE  y[m, n] = acc
+//   MM_LIN_RESID  resid[m, n] = resid[m, n] + round(acc)     (out_proj + residual,
+//                 mamba_model.py:48 -- the residual stream stays in x's dtype)
+//   MM_LIN_CONV   in_proj + conv window: for n < n_conv the rounded acc is the new
+//                 conv input x[m, n]: the (M, n_conv, 4) conv state shifts in place
+//                 and conv_out[m, n] = silu(bias + w . window) (mamba_block.py:
+//                 172-179); for n >= n_conv, y[m, n - n_conv] = acc (the z half).
+#include "mm_common.h"
+
+namespace mm {
+namespace gemm {
+
+constexpr int kTileN = 32;
+constexpr int kStepK = 16;
+constexpr int kChunkK = 64;               // K per LDS chunk = 4 MFMA steps
+constexpr int kSteps = kChunkK / kStepK;
+constexpr int kMaxM = 64;
+constexpr int kRowBytes = kChunkK * 2 + 16;  // padded LDS row of one X chunk
+constexpr int kXLds = kMaxM * kRowBytes;     // 9216 B per wave for the X chunk
+constexpr int kPartial = 3;                  // internal "epilogue": write fp32 partials
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+template <int DT>
+__device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (DT == MM_F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+struct LinParams {
+  const void* x;
+  const void* w;  // packed
+  void* y;
+  void* resid;
+  void* conv_state;
+  const void* conv_w;
+  const void* conv_b;
+  void* conv_out;
+  float* partials;  // split calls: [ks][M][N] fp32
+  int64_t M, N, K, ldx, ldy, ldr, ldc, n_conv;
+  int32_t ks;       // K splits across workgroups (grid.y)
+};
+
+struct Plan {
+  int nt, ks, ksw;
+};
+
+// Launch shape (from a sweep on MI355X over the decode shapes of Mamba-130M..2.8B):
+// NT = 2 n-tiles per wave once N has >= 256 32-column tiles.  With >= 128 column
+// tiles K stays in the workgroup, with up to 4 waves splitting it; below that, K is
+// split over single-wave workgroups until ~640 of them fill the chip, each keeping
+// >= 2 chunks of K.
+inline Plan plan(int64_t N, int64_t K) {
+  const int64_t nchunks = K / kChunkK;
+  Plan p{1, 1, 1};
+  if (ceil_div(N, kTileN) >= 256) p.nt = 2;
+  const int64_t ntiles = ceil_div(N, kTileN * p.nt);
+  if (ntiles >= 128) {
+    while (p.ksw < 4 && ntiles * p.ksw < 512 && nchunks / (p.ksw * 2) >= 2) p.ksw *= 2;
+  } else {
+    while (p.ks < 64 && ntiles * p.ks < 640 && nchunks / (p.ks * 2) >= 2) p.ks *= 2;
+  }
+  return p;
+}
+
+template <int DT, int EPI>
+__device__ __forceinline__ void epilogue(const LinParams& p, int64_t m, int64_t n, float v) {
+  using T = typename Ty<DT>::T;
+  if constexpr (EPI == MM_LIN_STORE) {
+    st<DT>(p.y, m * p.ldy + n, v);
+  } else if constexpr (EPI == MM_LIN_RESID) {
+    T* r = static_cast<T*>(p.resid) + m * p.ldr + n;
+    *r = Ty<DT>::from(Ty<DT>::f(*r) + Ty<DT>::f(Ty<DT>::from(v)));
+  } else {
+    if (n < p.n_conv) {
+      typedef T T4 __attribute__((ext_vector_type(4)));
+      T4* sp = static_cast<T4*>(p.conv_state) + m * p.n_conv + n;
+      const T4 win = *sp;
+      const T4 cw = static_cast<const T4*>(p.conv_w)[n];
+      const T xr = Ty<DT>::from(v);
+      float a = p.conv_b ? ld<DT>(p.conv_b, n) : 0.0f;
+      a = __builtin_fmaf(Ty<DT>::f(cw[0]), Ty<DT>::f(win[1]), a);
+      a = __builtin_fmaf(Ty<DT>::f(cw[1]), Ty<DT>::f(win[2]), a);
+      a = __builtin_fmaf(Ty<DT>::f(cw[2]), Ty<DT>::f(win[3]), a);
+      a = __builtin_fmaf(Ty<DT>::f(cw[3]), Ty<DT>::f(xr), a);
+      T4 nw;
+      nw[0] = win[1];
+      nw[1] = win[2];
+      nw[2] = win[3];
+      nw[3] = xr;
+      *sp = nw;
+      st<DT>(p.conv_out, m * p.ldc + n, silu_f(a));
+    } else {
+      st<DT>(p.y, m * p.ldy + (n - p.n_conv), v);
+    }
+  }
+}
+
+// MFMA output layout: lane l, register i of a 32x32 tile holds row
+// 8*(i/4) + 4*(l/32) + i%4, column l%32.
+__device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
+
+template <int DT, int KSW, int MT, int NT, int EPI>
+__global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
+  using T = typename Ty<DT>::T;
+  constexpr int XI = MT * 4;                 // X load instructions per chunk (8 rows each)
+  constexpr int NACC = MT * NT * 16;         // accumulator floats per lane
+  constexpr int kWaveLds = kXLds > NACC * 64 * 4 ? kXLds : NACC * 64 * 4;
+  constexpr int TN = NT * kTileN;            // columns per workgroup
+  __shared__ __align__(16) char smem[(EPI == kPartial ? 1 : KSW) * kWaveLds];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  char* const xs = smem + (EPI == kPartial ? 0 : wave * kWaveLds);
+  const int64_t t = blockIdx.x;
+  const int ks = blockIdx.y;
+  const int64_t n0 = t * TN;
+  const int64_t nsteps = p.K / kStepK;
+  const int64_t nchunks = p.K / kChunkK;
+  // chunk range of this workgroup, then of this wave
+  const int64_t per_wg = (nchunks + p.ks - 1) / p.ks;
+  const int64_t g0 = ks * per_wg;
+  const int64_t g1 = g0 + per_wg < nchunks ? g0 + per_wg : nchunks;
+  const int64_t per_w = (g1 - g0 + KSW - 1) / KSW;
+  const int64_t c_begin = g0 + wave * per_w;
+  const int64_t c_end = c_begin + per_w < g1 ? c_begin + per_w : g1;
+
+  // Every global load is unconditional and in bounds (chunks past this wave's range
+  // re-read its last chunk, rows past M read row 0, column tiles past N read tile 0
+  // -- all of which only feed outputs that are never stored), so the compiler
+  // counts outstanding loads exactly.
+  const int64_t ntiles32 = (p.N + kTileN - 1) / kTileN;
+  const u32x4* wp[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int64_t tj = t * NT + j;
+    wp[j] = static_cast<const u32x4*>(p.w) + (tj < ntiles32 ? tj : 0) * nsteps * 64 + lane;
+  }
+  const T* xrow[XI];
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int64_t r = 8 * i + (lane >> 3);
+    xrow[i] = static_cast<const T*>(p.x) + (r < p.M ? r : 0) * p.ldx + 8 * (lane & 7);
+  }
+  // LDS slots: write (row 8i + l/8, 16-byte column l%8); read for step g, m-tile mt:
+  // row 32mt + l%32, column 2g + l/32.
+  const int wr_off = (lane >> 3) * kRowBytes + (lane & 7) * 16;
+  const int rd_off = (lane & 31) * kRowBytes + (lane >> 5) * 16;
+
+  f32x16 acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mt][j][i] = 0.0f;
+
+  if (c_begin < c_end) {
+    const int64_t c_last = c_end - 1;
+    u32x4 wa[NT][kSteps], xa[XI], wb[NT][kSteps], xb[XI];
+    auto load = [&](u32x4(&wv)[NT][kSteps], u32x4(&xv)[XI], int64_t c) {
+      const int64_t cc = c < c_end ? c : c_last;
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int g = 0; g < kSteps; ++g) wv[j][g] = wp[j][(cc * kSteps + g) * 64];
+#pragma unroll
+      for (int i = 0; i < XI; ++i) xv[i] = *reinterpret_cast<const u32x4*>(xrow[i] + cc * kChunkK);
+    };
+    auto compute = [&](const u32x4(&wv)[NT][kSteps], const u32x4(&xv)[XI], int64_t c) {
+      if (c >= c_end) return;
+#pragma unroll
+      for (int i = 0; i < XI; ++i)
+        *reinterpret_cast<u32x4*>(xs + 8 * i * kRowBytes + wr_off) = xv[i];
+      // LDS is in order per wave: the reads below see the writes above; this only
+      // keeps the compiler from moving them across.
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int g = 0; g < kSteps; ++g)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(xs + mt * 32 * kRowBytes + rd_off + g * 32);
+#pragma unroll
+          for (int j = 0; j < NT; ++j) acc[mt][j] = mfma<DT>(a, wv[j][g], acc[mt][j]);
+        }
+      __builtin_amdgcn_wave_barrier();
+    };
+
+    load(wa, xa, c_begin);
+    for (int64_t c = c_begin; c < c_end; c += 2) {
+      load(wb, xb, c + 1);
+      compute(wa, xa, c);
+      load(wa, xa, c + 2);
+      compute(wb, xb, c + 1);
+    }
+  }
+
+  if constexpr (EPI == kPartial) {
+    // Single-wave workgroup: write the raw tile to partials[ks] (row-major), a row
+    // segment of 32 consecutive floats per half-wave and register.
+    float* const dst = p.partials + static_cast<int64_t>(ks) * p.M * p.N;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int64_t m = 32 * mt + acc_row(i, lane);
+          const int64_t n = n0 + 32 * j + (lane & 31);
+          if (m < p.M && n < p.N) dst[m * p.N + n] = acc[mt][j][i];
+        }
+    return;
+  } else {
+    // Partial tiles -> this wave's LDS slot (register-major, lane-contiguous).
+    float* const part = reinterpret_cast<float*>(xs);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) part[((mt * NT + j) * 16 + i) * 64 + lane] = acc[mt][j][i];
+    __syncthreads();
+    // Tile element e = row * TN + col, summed over the waves in order.  Each thread
+    // takes EPT elements; the epilogue's own loads (residual, conv window, conv
+    // weights) for all of them are issued before any of them is used.
+    constexpr int EPT = MT * 32 * TN / (KSW * 64);
+    float vals[EPT];
+    int64_t ms[EPT], ns[EPT];
+#pragma unroll
+    for (int u = 0; u < EPT; ++u) {
+      const int e = threadIdx.x + u * KSW * 64;
+      const int row = e / TN, col = e % TN;
+      const int rr = row & 31;
+      const int reg = (((row >> 5) * NT + (col >> 5)) * 16) + 4 * (rr >> 3) + (rr & 3);
+      const int ln = (col & 31) + 32 * ((rr >> 2) & 1);
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < KSW; ++w)
+        v += reinterpret_cast<const float*>(smem + w * kWaveLds)[reg * 64 + ln];
+      vals[u] = v;
+      ms[u] = row;
+      ns[u] = n0 + col;
+    }
+    if constexpr (EPI == MM_LIN_STORE) {
+#pragma unroll
+      for (int u = 0; u < EPT; ++u)
+        if (ms[u] < p.M && ns[u] < p.N) st<DT>(p.y, ms[u] * p.ldy + ns[u], vals[u]);
+    } else if constexpr (EPI == MM_LIN_RESID) {
+      T* const rb = static_cast<T*>(p.resid);
+      T old[EPT];
+#pragma unroll
+      for (int u = 0; u < EPT; ++u) {
+        const bool ok = ms[u] < p.M && ns[u] < p.N;
+        old[u] = rb[ok ? ms[u] * p.ldr + ns[u] : 0];
+      }
+#pragma unroll
+      for (int u = 0; u < EPT; ++u)
+        if (ms[u] < p.M && ns[u] < p.N)
+          rb[ms[u] * p.ldr + ns[u]] = Ty<DT>::from(Ty<DT>::f(old[u]) + Ty<DT>::f(Ty<DT>::from(vals[u])));
+    } else {
+      typedef T T4 __attribute__((ext_vector_type(4)));
+      T4* const sb = static_cast<T4*>(p.conv_state);
+      const T4* const wb = static_cast<const T4*>(p.conv_w);
+      const T* const bb = static_cast<const T*>(p.conv_b ? p.conv_b : p.conv_w);
+      T4 win[EPT], cw[EPT];
+      T bias[EPT];
+#pragma unroll
+      for (int u = 0; u < EPT; ++u) {
+        const bool ok = ms[u] < p.M && ns[u] < p.n_conv;
+        const int64_t mc = ok ? ms[u] : 0, nc = ok ? ns[u] : 0;
+        win[u] = sb[mc * p.n_conv + nc];
+        cw[u] = wb[nc];
+        bias[u] = bb[p.conv_b ? nc : 0];
+      }
+#pragma unroll
+      for (int u = 0; u < EPT; ++u) {
+        const int64_t m = ms[u], n = ns[u];
+        if (m >= p.M || n >= p.N) continue;
+        if (n < p.n_conv) {
+          const T xr = Ty<DT>::from(vals[u]);
+          float a = p.conv_b ? Ty<DT>::f(bias[u]) : 0.0f;
+          a = __builtin_fmaf(Ty<DT>::f(cw[u][0]), Ty<DT>::f(win[u][1]), a);
+          a = __builtin_fmaf(Ty<DT>::f(cw[u][1]), Ty<DT>::f(win[u][2]), a);
+          a = __builtin_fmaf(Ty<DT>::f(cw[u][2]), Ty<DT>::f(win[u][3]), a);
+          a = __builtin_fmaf(Ty<DT>::f(cw[u][3]), Ty<DT>::f(xr), a);
+          T4 nw;
+          nw[0] = win[u][1];
+          nw[1] = win[u][2];
+          nw[2] = win[u][3];
+          nw[3] = xr;
+          sb[m * p.n_conv + n] = nw;
+          st<DT>(p.conv_out, m * p.ldc + n, silu_f(a));
+        } else {
+          st<DT>(p.y, m * p.ldy + (n - p.n_conv), vals[u]);
+        }
+      }
+    }
+  }
+}
+
+// Split calls, second pass: y = sum over splits (in order) of the fp32 partials,
+// then the epilogue.  One thread per 4 consecutive columns of a row; the KS loads
+// of a thread are all issued before the sum (KS is a template parameter).
+template <int DT, int EPI, int KS>
+__global__ __launch_bounds__(256) void reduce_kernel(const LinParams p) {
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t nq = (p.N + 3) / 4;
+  if (q >= p.M * nq) return;
+  const int64_t m = q / nq, n = (q % nq) * 4;
+  const int64_t plane = p.M * p.N;
+  const float* src = p.partials + m * p.N + n;
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (n + 4 <= p.N && (p.N & 3) == 0) {
+    f32x4 a[KS];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) a[k] = *reinterpret_cast<const f32x4*>(src + k * plane);
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      v[0] += a[k][0];
+      v[1] += a[k][1];
+      v[2] += a[k][2];
+      v[3] += a[k][3];
+    }
+  } else {
+    for (int k = 0; k < KS; ++k)
+      for (int u = 0; u < 4; ++u)
+        if (n + u < p.N) v[u] += src[k * plane + u];
+  }
+  for (int u = 0; u < 4; ++u)
+    if (n + u < p.N) epilogue<DT, EPI>(p, m, n + u, v[u]);
+}
+
+// Packed layout: dst block (t, s), lane l = W[32t + l%32, 16s + 8(l/32) .. +7]
+// (zero rows past N).  One thread per 16-byte piece.
+template <int DT>
+__global__ __launch_bounds__(256) void pack_kernel(const void* __restrict__ w, u32x4* __restrict__ dst,
+                                                   int64_t N, int64_t K, int64_t ldw, int64_t total) {
+  using T = typename Ty<DT>::T;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int64_t nsteps = K / kStepK;
+  const int lane = static_cast<int>(i & 63);
+  const int64_t s = (i >> 6) % nsteps;
+  const int64_t t = (i >> 6) / nsteps;
+  const int64_t n = t * kTileN + (lane & 31);
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (n < N) v = *reinterpret_cast<const u32x4*>(static_cast<const T*>(w) + n * ldw + s * kStepK + 8 * (lane >> 5));
+  dst[i] = v;
+}
+
+template <int DT, int KSW, int MT, int NT>
+void launch_epi(const LinParams& p, int32_t epi, dim3 grid, hipStream_t s) {
+  const dim3 block(KSW * 64);
+  switch (epi) {
+    case MM_LIN_STORE:
+      hipLaunchKernelGGL((linear_kernel<DT, KSW, MT, NT, MM_LIN_STORE>), grid, block, 0, s, p);
+      break;
+    case MM_LIN_RESID:
+      hipLaunchKernelGGL((linear_kernel<DT, KSW, MT, NT, MM_LIN_RESID>), grid, block, 0, s, p);
+      break;
+    case MM_LIN_CONV:
+      hipLaunchKernelGGL((linear_kernel<DT, KSW, MT, NT, MM_LIN_CONV>), grid, block, 0, s, p);
+      break;
+    default:
+      hipLaunchKernelGGL((linear_kernel<DT, 1, MT, NT, kPartial>), grid, dim3(64), 0, s, p);
+      break;
+  }
+}
+
+template <int DT, int MT, int NT>
+void launch_ksw(const LinParams& p, int32_t epi, int ksw, dim3 grid, hipStream_t s) {
+  switch (ksw) {
+    case 1: launch_epi<DT, 1, MT, NT>(p, epi, grid, s); break;
+    case 2: launch_epi<DT, 2, MT, NT>(p, epi, grid, s); break;
+    default: launch_epi<DT, 4, MT, NT>(p, epi, grid, s); break;
+  }
+}
+
+template <int DT>
+void launch_main(const LinParams& p, int32_t epi, const Plan& pl, dim3 grid, hipStream_t s) {
+  const bool two = p.M > 32;
+  if (two && pl.nt == 2) launch_ksw<DT, 2, 2>(p, epi, pl.ksw, grid, s);
+  else if (two) launch_ksw<DT, 2, 1>(p, epi, pl.ksw, grid, s);
+  else if (pl.nt == 2) launch_ksw<DT, 1, 2>(p, epi, pl.ksw, grid, s);
+  else launch_ksw<DT, 1, 1>(p, epi, pl.ksw, grid, s);
+}
+
+template <int DT, int EPI>
+void launch_reduce_ks(const LinParams& p, dim3 grid, hipStream_t s) {
+  switch (p.ks) {
+    case 2: hipLaunchKernelGGL((reduce_kernel<DT, EPI, 2>), grid, dim3(256), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((reduce_kernel<DT, EPI, 4>), grid, dim3(256), 0, s, p); break;
+    case 8: hipLaunchKernelGGL((reduce_kernel<DT, EPI, 8>), grid, dim3(256), 0, s, p); break;
+    case 16: hipLaunchKernelGGL((reduce_kernel<DT, EPI, 16>), grid, dim3(256), 0, s, p); break;
+    case 32: hipLaunchKernelGGL((reduce_kernel<DT, EPI, 32>), grid, dim3(256), 0, s, p); break;
+    default: hipLaunchKernelGGL((reduce_kernel<DT, EPI, 64>), grid, dim3(256), 0, s, p); break;
+  }
+}
+
+template <int DT>
+void launch_reduce(const LinParams& p, int32_t epi, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(ceil_div(p.M * ceil_div(p.N, 4), 256)));
+  switch (epi) {
+    case MM_LIN_STORE: launch_reduce_ks<DT, MM_LIN_STORE>(p, grid, s); break;
+    case MM_LIN_RESID: launch_reduce_ks<DT, MM_LIN_RESID>(p, grid, s); break;
+    default: launch_reduce_ks<DT, MM_LIN_CONV>(p, grid, s); break;
+  }
+}
+
+}  // namespace gemm
+}  // namespace mm
+
+extern "C" {
+
+size_t mm_packed_linear_weight_bytes(int64_t N, int64_t K, int32_t dtype) {
+  using namespace mm;
+  if (N <= 0 || K <= 0 || !valid_dtype(dtype)) return 0;
+  return static_cast<size_t>(round_up(N, gemm::kTileN) * K * dtype_size(dtype));
+}
+
+int mm_pack_linear_weight(const void* w, void* packed, int64_t N, int64_t K, int64_t ldw,
+                          int32_t dtype, void* stream) {
+  using namespace mm;
+  using namespace mm::gemm;
+  clear_error();
+  if (!w || !packed) return fail(MM_ERR_NULL_POINTER, "w and packed are required");
+  if (N < 0 || K < 0) return fail(MM_ERR_SHAPE, "negative size");
+  if (dtype != MM_F16 && dtype != MM_BF16) return fail(MM_ERR_DTYPE, "dtype must be f16 or bf16");
+  if (K % kChunkK != 0 || ldw < K || ldw % 8 != 0 || !aligned(w, 16) || !aligned(packed, 16))
+    return fail(MM_ERR_LAYOUT, "K must be a multiple of %d, ldw >= K a multiple of 8, "
+                "w and packed 16-byte aligned", kChunkK);
+  if (N == 0 || K == 0) return MM_OK;
+  const int64_t total = ceil_div(N, kTileN) * (K / kStepK) * 64;
+  const dim3 grid(static_cast<unsigned>(ceil_div(total, 256)));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  u32x4* dst = static_cast<u32x4*>(packed);
+  if (dtype == MM_F16)
+    hipLaunchKernelGGL((pack_kernel<MM_F16>), grid, dim3(256), 0, s, w, dst, N, K, ldw, total);
+  else
+    hipLaunchKernelGGL((pack_kernel<MM_BF16>), grid, dim3(256), 0, s, w, dst, N, K, ldw, total);
+  return check_launch("pack_linear_weight");
+}
+
+size_t mm_decode_linear_workspace_size(int64_t M, int64_t N, int64_t K) {
+  using namespace mm;
+  using namespace mm::gemm;
+  if (M <= 0 || N <= 0 || K <= 0 || M > kMaxM || K % kChunkK != 0) return 0;
+  const Plan pl = plan(N, K);
+  if (pl.ks == 1) return 0;
+  return static_cast<size_t>(pl.ks * M * N * 4);
+}
+
+int mm_decode_linear(const mm_linear_params* prm, void* stream) {
+  using namespace mm;
+  using namespace mm::gemm;
+  clear_error();
+  if (!prm) return fail(MM_ERR_NULL_POINTER, "params is NULL");
+  const mm_linear_params& q = *prm;
+  if (!q.x || !q.w_packed) return fail(MM_ERR_NULL_POINTER, "x and w_packed are required");
+  if (q.M < 0 || q.N < 0 || q.K < 0) return fail(MM_ERR_SHAPE, "negative size");
+  if (q.M > kMaxM) return fail(MM_ERR_SHAPE, "M=%lld exceeds %d", (long long)q.M, kMaxM);
+  if (q.dtype != MM_F16 && q.dtype != MM_BF16)
+    return fail(MM_ERR_DTYPE, "dtype %d: the decode GEMM takes f16 or bf16", q.dtype);
+  if (q.epilogue != MM_LIN_STORE && q.epilogue != MM_LIN_RESID && q.epilogue != MM_LIN_CONV)
+    return fail(MM_ERR_SHAPE, "unknown epilogue %d", q.epilogue);
+  if (q.K % kChunkK != 0 || q.ldx < q.K || q.ldx % 8 != 0 || !aligned(q.x, 16) ||
+      !aligned(q.w_packed, 16))
+    return fail(MM_ERR_LAYOUT, "K must be a multiple of %d, ldx >= K a multiple of 8, x and "
+                "w_packed 16-byte aligned", kChunkK);
+  if (q.N > 0x7fffffffLL) return fail(MM_ERR_SHAPE, "N too large");
+  if (q.epilogue == MM_LIN_STORE && !q.y) return fail(MM_ERR_NULL_POINTER, "y is required");
+  if (q.epilogue == MM_LIN_RESID && !q.resid) return fail(MM_ERR_NULL_POINTER, "resid is required");
+  if (q.epilogue == MM_LIN_CONV) {
+    if (!q.conv_state || !q.conv_w || !q.conv_out || (!q.y && q.n_conv < q.N))
+      return fail(MM_ERR_NULL_POINTER, "conv_state, conv_w, conv_out and y are required");
+    if (q.n_conv < 0 || q.n_conv > q.N) return fail(MM_ERR_SHAPE, "n_conv outside [0, N]");
+    if (!aligned(q.conv_state, 8) || !aligned(q.conv_w, 8))
+      return fail(MM_ERR_LAYOUT, "conv_state and conv_w must be 8-byte aligned");
+  }
+  if (q.M == 0 || q.N == 0) return MM_OK;
+  const Plan pl = plan(q.N, q.K);
+  const size_t need = mm_decode_linear_workspace_size(q.M, q.N, q.K);
+  if (need > 0) {
+    if (!q.workspace || q.workspace_bytes < need)
+      return fail(MM_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need,
+                  q.workspace ? q.workspace_bytes : (size_t)0);
+    if (!aligned(q.workspace, 16)) return fail(MM_ERR_LAYOUT, "workspace must be 16-byte aligned");
+  }
+  LinParams p;
+  p.x = q.x;
+  p.w = q.w_packed;
+  p.y = q.y;
+  p.resid = q.resid;
+  p.conv_state = q.conv_state;
+  p.conv_w = q.conv_w;
+  p.conv_b = q.conv_b;
+  p.conv_out = q.conv_out;
+  p.partials = need ? static_cast<float*>(q.workspace) : nullptr;
+  p.M = q.M;
+  p.N = q.N;
+  p.K = q.K;
+  p.ldx = q.ldx;
+  p.ldy = q.ldy;
+  p.ldr = q.ldr;
+  p.ldc = q.ldc;
+  p.n_conv = q.n_conv;
+  p.ks = pl.ks;
+  const dim3 grid(static_cast<unsigned>(ceil_div(q.N, kTileN * pl.nt)), static_cast<unsigned>(pl.ks));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int32_t main_epi = pl.ks > 1 ? kPartial : q.epilogue;
+  if (q.dtype == MM_F16) {
+    launch_main<MM_F16>(p, main_epi, pl, grid, s);
+    if (pl.ks > 1) launch_reduce<MM_F16>(p, q.epilogue, s);
+  } else {
+    launch_main<MM_BF16>(p, main_epi, pl, grid, s);
+    if (pl.ks > 1) launch_reduce<MM_BF16>(p, q.epilogue, s);
+  }
+  return check_launch("decode_linear");
+}
+
+}  // extern "C"

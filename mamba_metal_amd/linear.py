@@ -1,0 +1,171 @@
+"""Decode-step projections on the weight-streaming GEMM (mm_decode_linear).
+
+At decode batch M <= 64 the nn.Linear layers of MambaBlock.step
+(mamba_metal/mamba_block.py:166-196) and the tied LM head (mamba_model.py:78)
+read each weight once and use it M times: HBM-bound on the weight bytes.  These
+wrappers run them on libmamba_mi355x's MFMA kernel, with the decode step's
+neighbouring element-wise ops folded into its epilogue:
+
+* ``decode_linear(x, w)``                  y = x @ w.T
+* ``decode_linear_resid_(resid, x, w)``    resid += round(x @ w.T)   (out_proj + residual add)
+* ``decode_in_proj_conv(x, w, conv_state, conv_w, conv_b, n_conv)``
+      xz = x @ w.T; the first n_conv columns go through the conv-window step
+      (state shifted in place, SiLU) -> (x_conv, z)
+
+``decode_linear_ok`` says whether a call fits the kernel (f16/bf16, M <= 64,
+16-byte aligned rows, K % 64 == 0); callers use torch's GEMM otherwise.
+
+The kernel reads W in a packed operand order: ``packed_weight(w)`` makes that copy
+once per weight (kept while the weight lives and is unchanged -- it doubles the
+decode weights' HBM footprint, 5.6 GB for Mamba-2.8B of 288 GB).  Narrow-N calls
+split K across workgroups through one fp32 partials workspace per device; calls are
+expected on one stream per device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import weakref
+
+import torch
+
+from mamba_metal_amd import _lib
+
+LIN_STORE, LIN_RESID, LIN_CONV = 0, 1, 2
+MAX_M = 64
+K_MULTIPLE = 64
+_WS_MIN = 8 << 20
+
+_PACKED: dict = {}    # id(w) -> (weakref to w, w._version, w.data_ptr(), packed copy)
+_WORKSPACES: dict = {}
+_RETIRED: list = []   # outgrown workspaces stay alive: captured graphs may hold them
+
+
+def _make_packed(w: torch.Tensor) -> torch.Tensor:
+    lib = _lib.load()
+    dev = _lib.require_cuda(w)
+    N, K = w.shape
+    code = _lib.dtype_code(w.dtype)
+    nbytes = lib.mm_packed_linear_weight_bytes(N, K, code)
+    packed = torch.empty(nbytes // w.element_size(), dtype=w.dtype, device=dev)
+    with torch.cuda.device(dev):
+        st = lib.mm_pack_linear_weight(w.data_ptr(), packed.data_ptr(), N, K, w.stride(0), code,
+                                       _lib.stream_of(dev))
+    _lib.check(st, "mm_pack_linear_weight")
+    return packed
+
+
+def packed_weight(w: torch.Tensor) -> torch.Tensor:
+    """The packed copy of an (N, K) f16/bf16 weight, made on first use and remade
+    when the weight changes in place; dropped when the weight is freed."""
+    key = id(w)
+    ent = _PACKED.get(key)
+    if ent is not None and ent[0]() is w and ent[1] == w._version and ent[2] == w.data_ptr():
+        return ent[3]
+    packed = _make_packed(w)
+    ref = weakref.ref(w, lambda _r, k=key: _PACKED.pop(k, None))
+    _PACKED[key] = (ref, w._version, w.data_ptr(), packed)
+    return packed
+
+
+def _workspace(dev, nbytes: int):
+    if nbytes == 0:
+        return None
+    ws = _WORKSPACES.get(dev)
+    if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED.append(ws)
+        ws = torch.empty(max(nbytes, _WS_MIN), dtype=torch.uint8, device=dev)
+        _WORKSPACES[dev] = ws
+    return ws
+
+
+def _rows_ok(t: torch.Tensor) -> bool:
+    es = t.element_size()
+    return (t.dim() == 2 and t.stride(1) == 1 and t.stride(0) % 8 == 0
+            and (t.data_ptr() % 16) == 0 and t.stride(0) >= t.shape[1] and es == 2)
+
+
+def decode_linear_ok(x: torch.Tensor, w: torch.Tensor) -> bool:
+    return (x.is_cuda and x.dtype in (torch.float16, torch.bfloat16) and w.dtype == x.dtype
+            and x.dim() == 2 and w.dim() == 2 and 1 <= x.shape[0] <= MAX_M
+            and x.shape[1] == w.shape[1] and x.shape[1] % K_MULTIPLE == 0
+            and _rows_ok(x) and _rows_ok(w))
+
+
+def _call(prm: _lib.LinearParams, dev) -> None:
+    lib = _lib.load()
+    ws = _workspace(dev, lib.mm_decode_linear_workspace_size(prm.M, prm.N, prm.K))
+    if ws is not None:
+        prm.workspace, prm.workspace_bytes = ws.data_ptr(), ws.numel()
+    with torch.cuda.device(dev):
+        st = lib.mm_decode_linear(ctypes.byref(prm), _lib.stream_of(dev))
+    _lib.check(st, "mm_decode_linear")
+
+
+def _base(x, w, epi) -> _lib.LinearParams:
+    if not decode_linear_ok(x, w):
+        raise ValueError("decode_linear: x (M<=64, K) and w (N, K) must be f16/bf16 of one "
+                         "dtype with unit inner stride, 16-byte aligned rows and K % 64 == 0")
+    prm = _lib.LinearParams()
+    prm.x, prm.w_packed = x.data_ptr(), packed_weight(w).data_ptr()
+    prm.M, prm.N, prm.K = x.shape[0], w.shape[0], x.shape[1]
+    prm.ldx = x.stride(0)
+    prm.dtype = _lib.dtype_code(x.dtype)
+    prm.epilogue = epi
+    return prm
+
+
+def decode_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None):
+    """y (M, N) = x (M, K) @ w (N, K).T"""
+    dev = _lib.require_cuda(x, w, out)
+    prm = _base(x, w, LIN_STORE)
+    if out is None:
+        out = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=dev)
+    if out.shape != (x.shape[0], w.shape[0]) or out.stride(1) != 1 or out.dtype != x.dtype:
+        raise ValueError("out must be (M, N) with x's dtype and unit inner stride")
+    prm.y, prm.ldy = out.data_ptr(), out.stride(0)
+    _call(prm, dev)
+    return out
+
+
+def decode_linear_resid_(resid: torch.Tensor, x: torch.Tensor, w: torch.Tensor):
+    """resid (M, N) += round(x @ w.T), in place in resid's (= x's) dtype."""
+    dev = _lib.require_cuda(resid, x, w)
+    prm = _base(x, w, LIN_RESID)
+    if resid.shape != (x.shape[0], w.shape[0]) or resid.stride(1) != 1 or resid.dtype != x.dtype:
+        raise ValueError("resid must be (M, N) with x's dtype and unit inner stride")
+    prm.resid, prm.ldr = resid.data_ptr(), resid.stride(0)
+    _call(prm, dev)
+    return resid
+
+
+def in_proj_conv_ok(x, w, conv_state, conv_w, conv_b) -> bool:
+    n_conv = conv_state.shape[1] if conv_state.dim() == 3 else -1
+    return (decode_linear_ok(x, w) and conv_state.dim() == 3 and conv_state.shape[2] == 4
+            and conv_state.dtype == x.dtype and conv_state.is_contiguous()
+            and conv_state.shape[0] == x.shape[0] and 0 < n_conv <= w.shape[0]
+            and conv_w.dtype == x.dtype and conv_w.is_contiguous() and conv_w.numel() == n_conv * 4
+            and (conv_b is None or (conv_b.dtype == x.dtype and conv_b.is_contiguous()))
+            and conv_state.data_ptr() % 8 == 0 and conv_w.data_ptr() % 8 == 0)
+
+
+def decode_in_proj_conv(x, w, conv_state, conv_w, conv_b=None):
+    """in_proj + decode conv-window step.  x (M, K); w (N, K) with N = n_conv + n_z;
+    conv_state (M, n_conv, 4) updated in place; conv_w (n_conv, 1, 4) or (n_conv, 4).
+    Returns (x_conv (M, n_conv) = silu(conv), z (M, n_z))."""
+    dev = _lib.require_cuda(x, w, conv_state, conv_w, conv_b)
+    if not in_proj_conv_ok(x, w, conv_state, conv_w, conv_b):
+        raise ValueError("decode_in_proj_conv: unsupported layout (see in_proj_conv_ok)")
+    prm = _base(x, w, LIN_CONV)
+    M, N = x.shape[0], w.shape[0]
+    n_conv = conv_state.shape[1]
+    x_conv = torch.empty((M, n_conv), dtype=x.dtype, device=dev)
+    z = torch.empty((M, N - n_conv), dtype=x.dtype, device=dev)
+    prm.y, prm.ldy = z.data_ptr(), z.stride(0)
+    prm.conv_state, prm.conv_w = conv_state.data_ptr(), conv_w.data_ptr()
+    prm.conv_b = _lib.ptr(conv_b)
+    prm.conv_out, prm.ldc = x_conv.data_ptr(), x_conv.stride(0)
+    prm.n_conv = n_conv
+    _call(prm, dev)
+    return x_conv, z

@@ -16,8 +16,9 @@ Where the reference transposes activations to (B, dim, L) contiguous copies
 before the scan (mamba_block.py:90-100), this block hands the kernel strided
 (B, L, dim) views: the scan reads channel-contiguous tiles directly.
 
-GEMMs (in/x/dt/out projections, tied LM head) run on torch (hipBLASLt); the
-conv, the scan and the decode state updates are libmamba_mi355x kernels.
+Prefill GEMMs (in/x/dt/out projections) run on torch (hipBLASLt); the conv, the
+scan and every decode-step op -- including the projections at decode batch <= 64,
+on the weight-streaming GEMM -- are libmamba_mi355x kernels.
 """
 
 from __future__ import annotations
@@ -29,7 +30,9 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from mamba_metal_amd.conv1d import causal_conv1d, conv_step
-from mamba_metal_amd.decode import ssm_step
+from mamba_metal_amd.decode import ssm_step_dtproj
+from mamba_metal_amd.linear import (decode_in_proj_conv, decode_linear, decode_linear_ok,
+                                    decode_linear_resid_, in_proj_conv_ok)
 from mamba_metal_amd.selective_scan import selective_scan_into
 
 
@@ -59,7 +62,16 @@ class MambaBlock(nn.Module):
 
     # ------------------------------------------------------------------ helpers
     def _A(self) -> torch.Tensor:
-        return -torch.exp(self.A_log.float())
+        """A = -exp(A_log) (float32), cached until A_log changes (decode would
+        otherwise spend two kernel launches per layer per token recomputing it)."""
+        key = (self.A_log.data_ptr(), self.A_log._version, self.A_log.device)
+        cache = getattr(self, "_A_cache", None)
+        if cache is None or cache[0] != key:
+            with torch.no_grad():
+                A = -torch.exp(self.A_log.detach().float())
+            self._A_cache = (key, A)
+            return A
+        return cache[1]
 
     def _split_xdbl(self, x_dbl):
         r, n = self.dt_rank, self.d_state
@@ -110,13 +122,38 @@ class MambaBlock(nn.Module):
         if not inplace:
             conv_state = conv_state.clone()
             ssm_state = ssm_state.clone()
+        return self.step_2d(x_token[:, 0, :], conv_state, ssm_state)[:, None, :], \
+            conv_state, ssm_state
+
+    def step_2d(self, x: torch.Tensor, conv_state: torch.Tensor, ssm_state: torch.Tensor,
+                resid: torch.Tensor | None = None):
+        """The decode step on a (B, d_model) row block, states updated in place.
+
+        in_proj GEMM + conv-window step -> x_proj GEMM -> fused dt_proj + softplus +
+        SSM update + C contraction + D skip + SiLU(z) -> out_proj GEMM.  For f16/bf16
+        at B <= 64 the GEMMs are the weight-streaming decode kernel with the conv
+        step folded into in_proj and, when ``resid`` is given, the residual add
+        folded into out_proj (the return value is then None: ``resid`` holds
+        x + out_proj(y)).  Otherwise the projections run on torch's GEMM."""
         di = self.d_inner
-        xz = self.in_proj(x_token[:, 0, :])                    # (B, 2*d_inner)
-        x_main, z = xz[:, :di], xz[:, di:]
-        x_conv = conv_step(conv_state, x_main, self.conv1d.weight, self.conv1d.bias,
-                           apply_silu=True)                    # (B, d_inner)
-        x_dbl = self.x_proj(x_conv)
+        W_in = self.in_proj.weight
+        if in_proj_conv_ok(x, W_in, conv_state, self.conv1d.weight, self.conv1d.bias):
+            x_conv, z = decode_in_proj_conv(x, W_in, conv_state, self.conv1d.weight,
+                                            self.conv1d.bias)
+        else:
+            xz = self.in_proj(x)                               # (B, 2*d_inner)
+            x_main, z = xz[:, :di], xz[:, di:]
+            x_conv = conv_step(conv_state, x_main, self.conv1d.weight, self.conv1d.bias,
+                               apply_silu=True)                # (B, d_inner)
+        W_x = self.x_proj.weight
+        x_dbl = decode_linear(x_conv, W_x) if decode_linear_ok(x_conv, W_x) else self.x_proj(x_conv)
         dt_pre, Bm, Cm = self._split_xdbl(x_dbl)
-        dt = F.linear(dt_pre, self.dt_proj.weight, self.dt_proj.bias)
-        y = ssm_step(ssm_state, x_conv, dt, self._A(), Bm, Cm, D=self.D, z=z, dt_softplus=True)
-        return self.out_proj(y)[:, None, :], conv_state, ssm_state
+        y = ssm_step_dtproj(ssm_state, x_conv, dt_pre, self.dt_proj.weight, self._A(), Bm, Cm,
+                            dt_bias=self.dt_proj.bias, D=self.D, z=z)
+        W_out = self.out_proj.weight
+        if decode_linear_ok(y, W_out):
+            if resid is not None and resid.dtype == y.dtype and resid.stride(-1) == 1:
+                decode_linear_resid_(resid, y, W_out)
+                return None
+            return decode_linear(y, W_out)
+        return self.out_proj(y)

@@ -13,8 +13,11 @@ from dataclasses import dataclass
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from mamba_metal_amd.mamba_block import MambaBlock
+from mamba_metal_amd.linear import decode_linear, decode_linear_ok
+from mamba_metal_amd.norm import add_rmsnorm
 
 
 @dataclass
@@ -66,15 +69,29 @@ class MambaModel(nn.Module):
     def d_inner(self) -> int:
         return self.cfg.expand * self.cfg.d_model
 
-    def _head(self, x):
-        return self.norm_f(x) @ self.embeddings.weight.T
+    def _head(self, h):
+        """Tied LM head on normalised rows: logits = h @ E^T (mamba_model.py:78).
+        Decode-sized row blocks run on the weight-streaming GEMM."""
+        E = self.embeddings.weight
+        if h.dim() == 2 and decode_linear_ok(h, E):
+            return decode_linear(h, E)
+        return F.linear(h, E)
+
+    def _run(self, input_ids, mix):
+        """Layer chain with the residual add fused into the next layer's RMSNorm:
+        resid += y_prev; h = RMSNorm(resid) (one kernel per layer boundary).
+        ``mix(mixer, h, resid)`` returns the mixer output, or None when it has
+        already added it into ``resid`` itself."""
+        resid = self.embeddings(input_ids)
+        y = None
+        for layer in self.layers:
+            h = add_rmsnorm(resid, y, layer.norm.weight, layer.norm.eps)
+            y = mix(layer.mixer, h, resid)
+        return add_rmsnorm(resid, y, self.norm_f.weight, self.norm_f.eps)
 
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
         """input_ids (B, L) -> logits (B, L, vocab_size)."""
-        x = self.embeddings(input_ids)
-        for layer in self.layers:
-            x = layer(x)
-        return self._head(x)
+        return self._head(self._run(input_ids, lambda m, h, resid: m(h)))
 
     def init_state(self, batch_size: int = 1):
         """Zero conv and SSM states (float32, as mamba_model.py:80-91)."""
@@ -90,27 +107,34 @@ class MambaModel(nn.Module):
 
         Returns (logits (B, L, vocab) -- (B, 1, vocab) with last_only=True --,
         conv_states, ssm_states)."""
-        x = self.embeddings(input_ids)
         convs, ssms = [], []
-        for layer in self.layers:
-            x, cs, ss = layer.prefill(x)
+
+        def mix(m, h, resid):
+            y, cs, ss = m.prefill(h)
             convs.append(cs)
             ssms.append(ss)
+            return y
+
+        h = self._run(input_ids, mix)
         if last_only:
-            x = x[:, -1:, :]
-        return self._head(x), convs, ssms
+            h = h[:, -1:, :]
+        return self._head(h), convs, ssms
 
     def step(self, input_ids: torch.Tensor, conv_states, ssm_states, inplace: bool = True):
         """One new token per sequence (B, 1) -> (logits (B, 1, vocab), states).
 
         States are updated in place and returned (see MambaBlock.step)."""
-        x = self.embeddings(input_ids.reshape(-1, 1))
-        new_conv, new_ssm = [], []
-        for layer, cs, ss in zip(self.layers, conv_states, ssm_states):
-            x, cs2, ss2 = layer.step(x, cs, ss, inplace=inplace)
-            new_conv.append(cs2)
-            new_ssm.append(ss2)
-        return self._head(x), new_conv, new_ssm
+        if not inplace:
+            conv_states = [t.clone() for t in conv_states]
+            ssm_states = [t.clone() for t in ssm_states]
+        it = iter(zip(conv_states, ssm_states))
+
+        def mix(m, h, resid):
+            cs, ss = next(it)
+            return m.step_2d(h, cs, ss, resid=resid)
+
+        h = self._run(input_ids.reshape(-1), mix)
+        return self._head(h)[:, None, :], list(conv_states), list(ssm_states)
 
 
 @torch.no_grad()

@@ -58,20 +58,22 @@ def test_single_hip_runtime_mapped(lib):
     assert len(_lib._hip_runtimes_mapped()) == 1
 
 
-def test_scan_params_layout_matches_header(tmp_path):
-    fields = [f for f, _ in _lib.ScanParams._fields_]
+@pytest.mark.parametrize("cname,cls", [("mm_scan_params", _lib.ScanParams),
+                                        ("mm_linear_params", _lib.LinearParams)])
+def test_params_layout_matches_header(tmp_path, cname, cls):
+    fields = [f for f, _ in cls._fields_]
     src = tmp_path / "off.c"
-    body = "\n".join(f'printf("{f} %zu\\n", offsetof(mm_scan_params, {f}));' for f in fields)
+    body = "\n".join(f'printf("{f} %zu\\n", offsetof({cname}, {f}));' for f in fields)
     src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "mamba_mi355x.h"\n'
-                   'int main(void){\n' + body + '\nprintf("sizeof %zu\\n", sizeof(mm_scan_params));'
+                   'int main(void){\n' + body + f'\nprintf("sizeof %zu\\n", sizeof({cname}));'
                    "return 0;}\n")
     exe = tmp_path / "off"
     subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
     got = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True,
                                                  check=True).stdout.splitlines())
     for f in fields:
-        assert int(got[f]) == getattr(_lib.ScanParams, f).offset, f
-    assert int(got["sizeof"]) == ctypes.sizeof(_lib.ScanParams)
+        assert int(got[f]) == getattr(cls, f).offset, f
+    assert int(got["sizeof"]) == ctypes.sizeof(cls)
 
 
 def _scan(lib, **over):
@@ -147,6 +149,59 @@ def test_conv_and_decode_validation(lib):
                                   1, 8, 16, 8, 8, 16, 16, 8, 8, 1, 1, None) == _lib.ERR_LAYOUT
     assert lib.mm_pair_scan(FAKE, FAKE, None, FAKE, -1, None) == _lib.ERR_SHAPE
     assert lib.mm_pair_scan(None, FAKE, None, FAKE, 4, None) == _lib.ERR_NULL_POINTER
+
+
+def test_fused_decode_and_norm_validation(lib):
+    """The fused decode step takes dstate 16, rank 1..256 and one dtype for x and W;
+    add_rmsnorm rejects negative sizes and eps < 0 -- all before any device access."""
+    def dtproj(dstate=16, rank=160, x_dtype=1, w_dtype=1, state=FAKE):
+        return lib.mm_decode_ssm_step_dtproj(state, FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE,
+                                             None, None, FAKE, 2, 64, dstate, rank, 64, 192, rank,
+                                             192, 192, 0, 64, x_dtype, w_dtype, None)
+    assert dtproj(dstate=8) == _lib.ERR_DSTATE
+    assert b"dstate" in lib.mm_last_error()
+    assert dtproj(rank=0) == _lib.ERR_SHAPE
+    assert dtproj(rank=257) == _lib.ERR_SHAPE
+    assert dtproj(w_dtype=0) == _lib.ERR_DTYPE
+    assert dtproj(state=FAKE + 4) == _lib.ERR_LAYOUT
+    assert lib.mm_add_rmsnorm(FAKE, None, FAKE, FAKE, -1, 8, 8, 8, 8, 1e-5, 1, 1, None) == _lib.ERR_SHAPE
+    assert lib.mm_add_rmsnorm(FAKE, None, FAKE, FAKE, 1, 8, 8, 8, 8, -1.0, 1, 1, None) == _lib.ERR_SHAPE
+    assert lib.mm_add_rmsnorm(None, None, FAKE, FAKE, 1, 8, 8, 8, 8, 1e-5, 1, 1, None) == \
+        _lib.ERR_NULL_POINTER
+
+
+def test_decode_linear_validation(lib):
+    """mm_decode_linear / mm_pack_linear_weight check shape, dtype, layout and the
+    workspace before touching memory."""
+    def call(**kw):
+        prm = _lib.LinearParams()
+        prm.x = prm.w_packed = prm.y = FAKE
+        prm.M, prm.N, prm.K = 4, 32, 64
+        prm.ldx, prm.ldy = 64, 32
+        prm.dtype, prm.epilogue = _lib.F16, 0
+        for k, v in kw.items():
+            setattr(prm, k, v)
+        return lib.mm_decode_linear(ctypes.byref(prm), None)
+    assert lib.mm_decode_linear(None, None) == _lib.ERR_NULL_POINTER
+    assert call(M=65) == _lib.ERR_SHAPE
+    assert call(dtype=_lib.F32) == _lib.ERR_DTYPE
+    assert call(K=48, ldx=48) == _lib.ERR_LAYOUT
+    assert call(ldx=32) == _lib.ERR_LAYOUT
+    assert call(x=FAKE + 8) == _lib.ERR_LAYOUT
+    assert call(epilogue=7) == _lib.ERR_SHAPE
+    assert call(epilogue=1) == _lib.ERR_NULL_POINTER          # RESID without resid
+    assert call(epilogue=2, n_conv=16) == _lib.ERR_NULL_POINTER
+    assert call(M=0) == _lib.OK and call(N=0) == _lib.OK
+    # narrow N splits K across workgroups: needs a workspace
+    need = lib.mm_decode_linear_workspace_size(64, 192, 5120)
+    assert need > 0
+    assert call(M=64, N=192, K=5120, ldx=5120) == _lib.ERR_WORKSPACE
+    assert call(M=64, N=192, K=5120, ldx=5120, workspace=FAKE, workspace_bytes=need - 1) == \
+        _lib.ERR_WORKSPACE
+    assert lib.mm_decode_linear_workspace_size(64, 50280, 2560) == 0   # wide N: no split
+    assert lib.mm_packed_linear_weight_bytes(50, 64, _lib.F16) == 64 * 64 * 2
+    assert lib.mm_pack_linear_weight(FAKE, FAKE, 50, 48, 48, _lib.F16, None) == _lib.ERR_LAYOUT
+    assert lib.mm_pack_linear_weight(FAKE, FAKE, 50, 64, 64, _lib.F32, None) == _lib.ERR_DTYPE
 
 
 def test_zero_sizes_are_noops(lib):

@@ -136,3 +136,26 @@ def test_bench_byte_formulas():
     assert bench.scan_bytes(1, 16, 16, 4096, xs=4, bcs=4) == 1_574_976  # config 0
     assert bench.decode_roofline_bytes(2560, 64, 50280, 16, 4, 160, 64) == pytest.approx(
         8_556_590_080, rel=2e-3)
+
+
+def test_packed_weight_cache(monkeypatch):
+    """The packed-weight cache: one pack per weight, a repack after an in-place
+    update, and the entry dropped with the weight."""
+    import gc
+
+    import torch
+
+    from mamba_metal_amd import linear
+
+    made = []
+    monkeypatch.setattr(linear, "_make_packed", lambda w: made.append(1) or w.clone())
+    w = torch.ones(4, 64)
+    p1 = linear.packed_weight(w)
+    assert linear.packed_weight(w) is p1 and len(made) == 1
+    w.mul_(2)
+    p2 = linear.packed_weight(w)
+    assert p2 is not p1 and len(made) == 2 and float(p2[0, 0]) == 2.0
+    n = len(linear._PACKED)
+    del w
+    gc.collect()
+    assert len(linear._PACKED) == n - 1

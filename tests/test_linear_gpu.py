@@ -1,0 +1,135 @@
+"""Decode-step GEMM (mm_decode_linear) against a float32 torch reference.
+
+The reference is x.float() @ w.float().T on the GPU (a plain fp32 GEMM of the same
+op); outputs are rounded once to f16/bf16, so the tolerance is the output dtype's
+half-ulp plus fp32 accumulation-order noise, relative to the output's scale."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close
+from oracle import numpy_ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
+
+
+def _ref(x, w):
+    return x.float() @ w.float().T
+
+
+def _check(got, ref, dtype, what):
+    scale = float(ref.abs().max()) + 1e-6
+    tol = TOL[dtype]
+    assert_close(got.float().cpu().numpy(), ref.cpu().numpy(), tol, tol * scale * 0.05, what)
+
+
+# decode shapes of Mamba-2.8B (in/out/x projections, head) and 130M, ragged M/N,
+# split-K (narrow N) and single-chunk K
+@pytest.mark.parametrize("M,K,N", [(64, 2560, 10240), (64, 5120, 2560), (64, 5120, 192),
+                                   (1, 768, 3072), (1, 1536, 80), (37, 1536, 100), (33, 256, 50),
+                                   (32, 64, 33), (64, 2560, 50280), (5, 64, 7), (64, 64, 4096)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_linear(dev, M, K, N, dtype):
+    from mamba_metal_amd.linear import decode_linear
+
+    g = torch.Generator(device=dev).manual_seed(M * 7 + K * 3 + N)
+    x = torch.randn((M, K), generator=g, device=dev).to(dtype)
+    w = (torch.randn((N, K), generator=g, device=dev) * 0.05).to(dtype)
+    y = decode_linear(x, w)
+    torch.cuda.synchronize()
+    _check(y, _ref(x, w), dtype, f"linear M={M} K={K} N={N}")
+    # deterministic: fixed-order split-K reduction
+    y2 = decode_linear(x, w)
+    assert torch.equal(y, y2)
+    # the split-K workspace is left zeroed: a third call on other data is right too
+    x3 = torch.randn((M, K), generator=g, device=dev).to(dtype)
+    _check(decode_linear(x3, w), _ref(x3, w), dtype, f"linear again M={M} K={K} N={N}")
+
+
+def test_decode_linear_split_sequence(dev):
+    """Split-K calls of different shapes in a row share one partials workspace; each
+    must be right whatever the previous call left there."""
+    from mamba_metal_amd.linear import decode_linear
+
+    g = torch.Generator(device=dev).manual_seed(11)
+    for (M, K, N) in [(64, 5120, 192), (1, 768, 3072), (64, 5120, 192), (33, 1536, 2000)]:
+        x = torch.randn((M, K), generator=g, device=dev).half()
+        w = (torch.randn((N, K), generator=g, device=dev) * 0.05).half()
+        _check(decode_linear(x, w), _ref(x, w), torch.float16, f"sequence M={M} K={K} N={N}")
+
+
+def test_packed_weight_refreshes_on_update(dev):
+    """The packed copy follows in-place weight updates (version counter)."""
+    from mamba_metal_amd.linear import decode_linear
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn((8, 128), generator=g, device=dev).half()
+    w = (torch.randn((64, 128), generator=g, device=dev) * 0.05).half()
+    decode_linear(x, w)
+    with torch.no_grad():
+        w.mul_(-2.0)
+    _check(decode_linear(x, w), _ref(x, w), torch.float16, "after update")
+
+
+def test_decode_linear_strided_rows(dev):
+    """x as a column slice of a wider buffer (row stride > K), y into a wider buffer."""
+    from mamba_metal_amd.linear import decode_linear
+
+    g = torch.Generator(device=dev).manual_seed(1)
+    big = torch.randn((40, 1024 + 64), generator=g, device=dev).half()
+    x = big[:, 64:]                                       # 16-byte aligned, stride 1088
+    w = (torch.randn((300, 1024), generator=g, device=dev) * 0.05).half()
+    outbuf = torch.zeros((40, 320), device=dev, dtype=torch.float16)
+    y = decode_linear(x, w, out=outbuf[:, :300])
+    _check(y, _ref(x, w), torch.float16, "strided")
+    assert torch.count_nonzero(outbuf[:, 300:]) == 0      # nothing written past N
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_linear_resid(dev, dtype):
+    from mamba_metal_amd.linear import decode_linear_resid_
+
+    g = torch.Generator(device=dev).manual_seed(2)
+    M, K, N = 64, 5120, 2560
+    y = torch.randn((M, K), generator=g, device=dev).to(dtype)
+    w = (torch.randn((N, K), generator=g, device=dev) * 0.02).to(dtype)
+    resid = torch.randn((M, N), generator=g, device=dev).to(dtype)
+    r0 = resid.float().cpu().numpy()
+    yr = _ref(y, w).to(dtype).float().cpu().numpy()
+    expect = (r0 + yr).astype(np.float64)
+    decode_linear_resid_(resid, y, w)
+    # resid + y cancels: the bound scales with the operands, not with the sum (one
+    # rounding of y and one of the sum, each a fraction of |operand|).
+    err = np.abs(resid.float().cpu().numpy() - expect)
+    bound = TOL[dtype] * (np.abs(r0) + np.abs(yr)) + 1e-6
+    assert (err <= bound).all(), f"resid: worst excess {float((err - bound).max()):.3e}"
+
+
+@pytest.mark.parametrize("M", [64, 3])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_in_proj_conv(dev, M, dtype):
+    """in_proj + conv-window step == GEMM, then the oracle's decode conv step."""
+    from mamba_metal_amd.linear import decode_in_proj_conv
+
+    g = torch.Generator(device=dev).manual_seed(3 + M)
+    K, di = 768, 1536
+    x = torch.randn((M, K), generator=g, device=dev).to(dtype)
+    w = (torch.randn((2 * di, K), generator=g, device=dev) * 0.05).to(dtype)
+    cw = torch.randn((di, 1, 4), generator=g, device=dev).to(dtype)
+    cb = torch.randn((di,), generator=g, device=dev).to(dtype)
+    st = torch.randn((M, di, 4), generator=g, device=dev).to(dtype)
+    st0 = st.clone()
+    x_conv, z = decode_in_proj_conv(x, w, st, cw, cb)
+    xz = _ref(x, w).to(dtype)                              # the rounded projection
+    _check(z, xz[:, di:].float(), dtype, "z")
+    ref, ref_st = numpy_ref.decode_conv_step(st0.float().cpu().numpy().astype(np.float64),
+                                             xz[:, :di].float().cpu().numpy().astype(np.float64),
+                                             cw.float().cpu().numpy()[:, 0].astype(np.float64),
+                                             cb.float().cpu().numpy().astype(np.float64))
+    tol = TOL[dtype]
+    # an input that lands on a rounding boundary may differ by one ulp of dtype
+    assert_close(x_conv.float().cpu().numpy(), ref, tol * 4, tol * 4, "x_conv")
+    assert_close(st.float().cpu().numpy(), ref_st, tol, tol * 4, "conv state")
