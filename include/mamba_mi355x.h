@@ -207,6 +207,10 @@ int mm_add_rmsnorm(void* resid, const void* add, const void* weight, void* out, 
  * epilogue MM_LIN_STORE: y[m, n] = acc.
  * epilogue MM_LIN_RESID: resid[m, n] = resid[m, n] + round(acc)  (out_proj followed
  *   by the residual add of mamba_model.py:48; y unused).
+ * epilogue MM_LIN_RESID_NORM: as MM_LIN_RESID, then the next RMSNorm of the updated
+ *   rows (mamba_model.py:40,48,69): norm_out[m, :] = resid[m, :] *
+ *   rsqrt(mean(resid[m, :]^2) + eps) * norm_w (norm_w in dtype; one launch fewer
+ *   than RESID + mm_add_rmsnorm).
  * epilogue MM_LIN_CONV:  in_proj followed by the conv-window step of
  *   mamba_block.py:172-179 on columns [0, n_conv): x = round(acc); conv_state
  *   (M, n_conv, 4) contiguous shifts in place; conv_out[m, n] = silu(conv_b[n] +
@@ -220,7 +224,8 @@ int mm_add_rmsnorm(void* resid, const void* add, const void* weight, void* out, 
 typedef enum mm_linear_epilogue {
   MM_LIN_STORE = 0,
   MM_LIN_RESID = 1,
-  MM_LIN_CONV = 2
+  MM_LIN_CONV = 2,
+  MM_LIN_RESID_NORM = 3
 } mm_linear_epilogue;
 
 typedef struct mm_linear_params {
@@ -232,11 +237,14 @@ typedef struct mm_linear_params {
   const void* conv_w;     /* CONV: (n_conv, 4) contiguous */
   const void* conv_b;     /* CONV: (n_conv,) or NULL */
   void* conv_out;         /* CONV: (M, n_conv) row stride ldc */
+  const void* norm_w;     /* RESID_NORM: (N,) */
+  void* norm_out;         /* RESID_NORM: (M, N) row stride ldn */
   void* workspace;        /* split-K counters + partial tiles (may be NULL if size 0) */
   size_t workspace_bytes;
   int64_t M, N, K;
-  int64_t ldx, ldy, ldr, ldc;
+  int64_t ldx, ldy, ldr, ldc, ldn;
   int64_t n_conv;
+  float eps;              /* RESID_NORM */
   int32_t dtype;          /* MM_F16 or MM_BF16 */
   int32_t epilogue;       /* mm_linear_epilogue */
 } mm_linear_params;

@@ -64,11 +64,11 @@ class LinearParams(ctypes.Structure):
 
     _fields_ = [
         ("x", _vp), ("w_packed", _vp), ("y", _vp), ("resid", _vp), ("conv_state", _vp),
-        ("conv_w", _vp), ("conv_b", _vp), ("conv_out", _vp), ("workspace", _vp),
-        ("workspace_bytes", _sz),
+        ("conv_w", _vp), ("conv_b", _vp), ("conv_out", _vp), ("norm_w", _vp), ("norm_out", _vp),
+        ("workspace", _vp), ("workspace_bytes", _sz),
         ("M", _i64), ("N", _i64), ("K", _i64),
-        ("ldx", _i64), ("ldy", _i64), ("ldr", _i64), ("ldc", _i64),
-        ("n_conv", _i64), ("dtype", _i32), ("epilogue", _i32),
+        ("ldx", _i64), ("ldy", _i64), ("ldr", _i64), ("ldc", _i64), ("ldn", _i64),
+        ("n_conv", _i64), ("eps", ctypes.c_float), ("dtype", _i32), ("epilogue", _i32),
     ]
 
 

@@ -227,14 +227,28 @@ __global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_dtproj_kernel(const
   const int64_t cc = cok ? c : 0;
   const T* const zp = static_cast<const T*>(p.z ? p.z : p.x);
 
-  float4 hv[kFusedBB];
-  T xr[kFusedBB], zr[kFusedBB];
+  // Load order matters (the load counter is in order): dt_in rows, B and C first
+  // (they gate the LDS staging and the barrier), then W, A, bias and D (needed by
+  // every row), then the state rows: each row's update and store can start as soon
+  // as its own state has arrived.
+  constexpr int NDT = (kFusedBB * 4 * RQ + NT - 1) / NT;
+  T dtr[NDT];
 #pragma unroll
-  for (int bb = 0; bb < kFusedBB; ++bb) {
-    const int64_t b = b0 + (bb < nb ? bb : 0);
-    hv[bb] = *reinterpret_cast<const float4*>(p.h + (b * p.dim + cc) * kFusedNS + q * 4);
-    xr[bb] = static_cast<const T*>(p.x)[b * p.xsb + cc];
-    zr[bb] = zp[p.z ? b * p.zsb + cc : b * p.xsb + cc];
+  for (int u = 0; u < NDT; ++u) {
+    const int e = tid + u * NT;
+    const int bb = e / (4 * RQ), r = e % (4 * RQ);
+    const bool ok = e < kFusedBB * 4 * RQ && bb < nb && r < R;
+    dtr[u] = static_cast<const T*>(p.dt_in)[ok ? (b0 + bb) * p.dtsb + r : 0];
+  }
+  constexpr int NBC = (kFusedBB * kFusedNS + NT - 1) / NT;
+  T br[NBC], cr[NBC];
+#pragma unroll
+  for (int u = 0; u < NBC; ++u) {
+    const int e = tid + u * NT;
+    const int bb = e / kFusedNS, n = e % kFusedNS;
+    const bool ok = e < kFusedBB * kFusedNS && bb < nb;
+    br[u] = static_cast<const T*>(p.B)[ok ? (b0 + bb) * p.Bsb + n : 0];
+    cr[u] = static_cast<const T*>(p.C)[ok ? (b0 + bb) * p.Csb + n : 0];
   }
   // This lane's slice of W[c, :] (zero beyond rank).
   const int r0 = q * RQ;
@@ -263,27 +277,16 @@ __global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_dtproj_kernel(const
   float4 Av = *reinterpret_cast<const float4*>(p.A + cc * kFusedNS + q * 4);
   const T biasr = static_cast<const T*>(p.bias ? p.bias : p.x)[p.bias ? cc : 0];
   const float Dr = p.D ? p.D[cc] : 0.0f;
+  float4 hv[kFusedBB];
+  T xr[kFusedBB], zr[kFusedBB];
+#pragma unroll
+  for (int bb = 0; bb < kFusedBB; ++bb) {
+    const int64_t b = b0 + (bb < nb ? bb : 0);
+    hv[bb] = *reinterpret_cast<const float4*>(p.h + (b * p.dim + cc) * kFusedNS + q * 4);
+    xr[bb] = static_cast<const T*>(p.x)[b * p.xsb + cc];
+    zr[bb] = zp[p.z ? b * p.zsb + cc : b * p.xsb + cc];
+  }
 
-  // dt_in rows, B and C of the batch block -> LDS (zero past rank / batch).
-  constexpr int NDT = (kFusedBB * 4 * RQ + NT - 1) / NT;
-  T dtr[NDT];
-#pragma unroll
-  for (int u = 0; u < NDT; ++u) {
-    const int e = tid + u * NT;
-    const int bb = e / (4 * RQ), r = e % (4 * RQ);
-    const bool ok = e < kFusedBB * 4 * RQ && bb < nb && r < R;
-    dtr[u] = static_cast<const T*>(p.dt_in)[ok ? (b0 + bb) * p.dtsb + r : 0];
-  }
-  constexpr int NBC = (kFusedBB * kFusedNS + NT - 1) / NT;
-  T br[NBC], cr[NBC];
-#pragma unroll
-  for (int u = 0; u < NBC; ++u) {
-    const int e = tid + u * NT;
-    const int bb = e / kFusedNS, n = e % kFusedNS;
-    const bool ok = e < kFusedBB * kFusedNS && bb < nb;
-    br[u] = static_cast<const T*>(p.B)[ok ? (b0 + bb) * p.Bsb + n : 0];
-    cr[u] = static_cast<const T*>(p.C)[ok ? (b0 + bb) * p.Csb + n : 0];
-  }
 #pragma unroll
   for (int u = 0; u < NDT; ++u) {
     const int e = tid + u * NT;

@@ -45,7 +45,7 @@ constexpr int kSteps = kChunkK / kStepK;
 constexpr int kMaxM = 64;
 constexpr int kRowBytes = kChunkK * 2 + 16;  // padded LDS row of one X chunk
 constexpr int kXLds = kMaxM * kRowBytes;     // 9216 B per wave for the X chunk
-constexpr int kPartial = 3;                  // internal "epilogue": write fp32 partials
+constexpr int kPartial = 4;                  // internal "epilogue": write fp32 partials
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -72,8 +72,11 @@ struct LinParams {
   const void* conv_w;
   const void* conv_b;
   void* conv_out;
+  const void* norm_w;
+  void* norm_out;
   float* partials;  // split calls: [ks][M][N] fp32
-  int64_t M, N, K, ldx, ldy, ldr, ldc, n_conv;
+  int64_t M, N, K, ldx, ldy, ldr, ldc, ldn, n_conv;
+  float eps;
   int32_t ks;       // K splits across workgroups (grid.y)
 };
 
@@ -365,6 +368,67 @@ __global__ __launch_bounds__(256) void reduce_kernel(const LinParams p) {
     if (n + u < p.N) epilogue<DT, EPI>(p, m, n + u, v[u]);
 }
 
+// Split calls with MM_LIN_RESID_NORM, second pass: one workgroup per row sums the
+// splits (in order), updates the residual row and writes its RMSNorm.  Thread t
+// takes float4 column groups t, t + 256, ...; all loads (partials, residual, norm
+// weight) are issued before the first sum.
+template <int DT, int KS, int CPT>
+__global__ __launch_bounds__(256) void reduce_norm_kernel(const LinParams p) {
+  using T = typename Ty<DT>::T;
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  __shared__ float s_part[4];
+  const int64_t m = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t ng = p.N / 4;
+  const int64_t plane = p.M * p.N;
+  T4* const rrow = reinterpret_cast<T4*>(static_cast<T*>(p.resid) + m * p.ldr);
+  const T4* const wrow = static_cast<const T4*>(p.norm_w);
+  f32x4 part[CPT][KS];
+  T4 rv[CPT], wv[CPT];
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const int64_t g = tid + 256 * u < ng ? tid + 256 * u : 0;
+#pragma unroll
+    for (int k = 0; k < KS; ++k)
+      part[u][k] = *reinterpret_cast<const f32x4*>(p.partials + k * plane + m * p.N + 4 * g);
+    rv[u] = rrow[g];
+    wv[u] = wrow[g];
+  }
+  float nv[CPT][4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const bool ok = tid + 256 * u < ng;
+    T4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float a = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) a += part[u][k][e];
+      const T r = Ty<DT>::from(Ty<DT>::f(rv[u][e]) + Ty<DT>::f(Ty<DT>::from(a)));
+      o[e] = r;
+      nv[u][e] = ok ? Ty<DT>::f(r) : 0.0f;
+      ss = __builtin_fmaf(nv[u][e], nv[u][e], ss);
+    }
+    if (ok) rrow[tid + 256 * u] = o;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  if ((tid & 63) == 0) s_part[tid >> 6] = ss;
+  __syncthreads();
+  const float inv = rsqrtf((s_part[0] + s_part[1] + s_part[2] + s_part[3]) / static_cast<float>(p.N) + p.eps);
+  T4* const orow = reinterpret_cast<T4*>(static_cast<T*>(p.norm_out) + m * p.ldn);
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    if (tid + 256 * u < ng) {
+      T4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = Ty<DT>::from(nv[u][e] * inv * Ty<DT>::f(wv[u][e]));
+      orow[tid + 256 * u] = o;
+    }
+  }
+}
+
 // Packed layout: dst block (t, s), lane l = W[32t + l%32, 16s + 8(l/32) .. +7]
 // (zero rows past N).  One thread per 16-byte piece.
 template <int DT>
@@ -442,6 +506,36 @@ void launch_reduce(const LinParams& p, int32_t epi, hipStream_t s) {
   }
 }
 
+template <int DT, int KS>
+void launch_reduce_norm_ks(const LinParams& p, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(p.M));
+  const int64_t ng = p.N / 4;
+  if (ng <= 256) hipLaunchKernelGGL((reduce_norm_kernel<DT, KS, 1>), grid, dim3(256), 0, s, p);
+  else if (ng <= 512) hipLaunchKernelGGL((reduce_norm_kernel<DT, KS, 2>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((reduce_norm_kernel<DT, KS, 4>), grid, dim3(256), 0, s, p);
+}
+
+template <int DT>
+void launch_reduce_norm(const LinParams& p, hipStream_t s) {
+  switch (p.ks) {
+    case 2: launch_reduce_norm_ks<DT, 2>(p, s); break;
+    case 4: launch_reduce_norm_ks<DT, 4>(p, s); break;
+    case 8: launch_reduce_norm_ks<DT, 8>(p, s); break;
+    default: launch_reduce_norm_ks<DT, 16>(p, s); break;
+  }
+}
+
+// The fused reduce + residual + RMSNorm pass covers split calls with <= 16 splits,
+// N % 4 == 0, N <= 4096 and 8-byte aligned rows; otherwise the RESID epilogue runs
+// and the norm follows as mm_add_rmsnorm.
+inline bool fused_norm_ok(const LinParams& p, int32_t dtype, const void* resid, const void* norm_w,
+                          const void* norm_out) {
+  const int64_t vb = 4 * dtype_size(dtype);
+  return p.ks > 1 && p.ks <= 16 && p.N % 4 == 0 && p.N <= 4096 && aligned(resid, vb) &&
+         aligned(norm_w, vb) && aligned(norm_out, vb) && (p.ldr * dtype_size(dtype)) % vb == 0 &&
+         (p.ldn * dtype_size(dtype)) % vb == 0;
+}
+
 }  // namespace gemm
 }  // namespace mm
 
@@ -496,7 +590,8 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
   if (q.M > kMaxM) return fail(MM_ERR_SHAPE, "M=%lld exceeds %d", (long long)q.M, kMaxM);
   if (q.dtype != MM_F16 && q.dtype != MM_BF16)
     return fail(MM_ERR_DTYPE, "dtype %d: the decode GEMM takes f16 or bf16", q.dtype);
-  if (q.epilogue != MM_LIN_STORE && q.epilogue != MM_LIN_RESID && q.epilogue != MM_LIN_CONV)
+  if (q.epilogue != MM_LIN_STORE && q.epilogue != MM_LIN_RESID && q.epilogue != MM_LIN_CONV &&
+      q.epilogue != MM_LIN_RESID_NORM)
     return fail(MM_ERR_SHAPE, "unknown epilogue %d", q.epilogue);
   if (q.K % kChunkK != 0 || q.ldx < q.K || q.ldx % 8 != 0 || !aligned(q.x, 16) ||
       !aligned(q.w_packed, 16))
@@ -504,7 +599,12 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
                 "w_packed 16-byte aligned", kChunkK);
   if (q.N > 0x7fffffffLL) return fail(MM_ERR_SHAPE, "N too large");
   if (q.epilogue == MM_LIN_STORE && !q.y) return fail(MM_ERR_NULL_POINTER, "y is required");
-  if (q.epilogue == MM_LIN_RESID && !q.resid) return fail(MM_ERR_NULL_POINTER, "resid is required");
+  if ((q.epilogue == MM_LIN_RESID || q.epilogue == MM_LIN_RESID_NORM) && !q.resid)
+    return fail(MM_ERR_NULL_POINTER, "resid is required");
+  if (q.epilogue == MM_LIN_RESID_NORM) {
+    if (!q.norm_w || !q.norm_out) return fail(MM_ERR_NULL_POINTER, "norm_w and norm_out are required");
+    if (!(q.eps >= 0.0f)) return fail(MM_ERR_SHAPE, "eps must be >= 0");
+  }
   if (q.epilogue == MM_LIN_CONV) {
     if (!q.conv_state || !q.conv_w || !q.conv_out || (!q.y && q.n_conv < q.N))
       return fail(MM_ERR_NULL_POINTER, "conv_state, conv_w, conv_out and y are required");
@@ -530,6 +630,10 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
   p.conv_w = q.conv_w;
   p.conv_b = q.conv_b;
   p.conv_out = q.conv_out;
+  p.norm_w = q.norm_w;
+  p.norm_out = q.norm_out;
+  p.ldn = q.ldn;
+  p.eps = q.eps;
   p.partials = need ? static_cast<float*>(q.workspace) : nullptr;
   p.M = q.M;
   p.N = q.N;
@@ -542,13 +646,24 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
   p.ks = pl.ks;
   const dim3 grid(static_cast<unsigned>(ceil_div(q.N, kTileN * pl.nt)), static_cast<unsigned>(pl.ks));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int32_t main_epi = pl.ks > 1 ? kPartial : q.epilogue;
+  const bool norm = q.epilogue == MM_LIN_RESID_NORM;
+  const bool fused_norm = norm && fused_norm_ok(p, q.dtype, q.resid, q.norm_w, q.norm_out);
+  const int32_t epi = norm ? MM_LIN_RESID : q.epilogue;  // RESID_NORM = RESID + norm pass
+  const int32_t main_epi = pl.ks > 1 ? kPartial : epi;
   if (q.dtype == MM_F16) {
     launch_main<MM_F16>(p, main_epi, pl, grid, s);
-    if (pl.ks > 1) launch_reduce<MM_F16>(p, q.epilogue, s);
+    if (fused_norm) launch_reduce_norm<MM_F16>(p, s);
+    else if (pl.ks > 1) launch_reduce<MM_F16>(p, epi, s);
   } else {
     launch_main<MM_BF16>(p, main_epi, pl, grid, s);
-    if (pl.ks > 1) launch_reduce<MM_BF16>(p, q.epilogue, s);
+    if (fused_norm) launch_reduce_norm<MM_BF16>(p, s);
+    else if (pl.ks > 1) launch_reduce<MM_BF16>(p, epi, s);
+  }
+  if (norm && !fused_norm) {
+    const int st = check_launch("decode_linear");
+    if (st != MM_OK) return st;
+    return mm_add_rmsnorm(q.resid, nullptr, q.norm_w, q.norm_out, q.M, q.N, q.ldr, 0, q.ldn, q.eps,
+                          q.dtype, q.dtype, stream);
   }
   return check_launch("decode_linear");
 }

@@ -8,6 +8,8 @@ neighbouring element-wise ops folded into its epilogue:
 
 * ``decode_linear(x, w)``                  y = x @ w.T
 * ``decode_linear_resid_(resid, x, w)``    resid += round(x @ w.T)   (out_proj + residual add)
+* ``decode_linear_resid_norm_(resid, x, w, norm_w, eps)``
+      the same, then returns RMSNorm(resid) * norm_w (the next layer's input)
 * ``decode_in_proj_conv(x, w, conv_state, conv_w, conv_b, n_conv)``
       xz = x @ w.T; the first n_conv columns go through the conv-window step
       (state shifted in place, SiLU) -> (x_conv, z)
@@ -31,7 +33,7 @@ import torch
 
 from mamba_metal_amd import _lib
 
-LIN_STORE, LIN_RESID, LIN_CONV = 0, 1, 2
+LIN_STORE, LIN_RESID, LIN_CONV, LIN_RESID_NORM = 0, 1, 2, 3
 MAX_M = 64
 K_MULTIPLE = 64
 _WS_MIN = 8 << 20
@@ -138,6 +140,23 @@ def decode_linear_resid_(resid: torch.Tensor, x: torch.Tensor, w: torch.Tensor):
     prm.resid, prm.ldr = resid.data_ptr(), resid.stride(0)
     _call(prm, dev)
     return resid
+
+
+def decode_linear_resid_norm_(resid: torch.Tensor, x: torch.Tensor, w: torch.Tensor,
+                              norm_w: torch.Tensor, eps: float, out: torch.Tensor | None = None):
+    """resid += round(x @ w.T) in place; returns RMSNorm(resid) * norm_w (M, N)."""
+    dev = _lib.require_cuda(resid, x, w, norm_w, out)
+    prm = _base(x, w, LIN_RESID_NORM)
+    if resid.shape != (x.shape[0], w.shape[0]) or resid.stride(1) != 1 or resid.dtype != x.dtype:
+        raise ValueError("resid must be (M, N) with x's dtype and unit inner stride")
+    if norm_w.shape != (w.shape[0],) or norm_w.dtype != x.dtype or not norm_w.is_contiguous():
+        raise ValueError("norm_w must be a contiguous (N,) vector in x's dtype")
+    if out is None:
+        out = torch.empty_like(resid)
+    prm.resid, prm.ldr = resid.data_ptr(), resid.stride(0)
+    prm.norm_w, prm.norm_out, prm.ldn, prm.eps = norm_w.data_ptr(), out.data_ptr(), out.stride(0), eps
+    _call(prm, dev)
+    return out
 
 
 def in_proj_conv_ok(x, w, conv_state, conv_w, conv_b) -> bool:

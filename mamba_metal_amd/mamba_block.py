@@ -32,7 +32,8 @@ import torch.nn.functional as F
 from mamba_metal_amd.conv1d import causal_conv1d, conv_step
 from mamba_metal_amd.decode import ssm_step_dtproj
 from mamba_metal_amd.linear import (decode_in_proj_conv, decode_linear, decode_linear_ok,
-                                    decode_linear_resid_, in_proj_conv_ok)
+                                    decode_linear_resid_, decode_linear_resid_norm_,
+                                    in_proj_conv_ok)
 from mamba_metal_amd.selective_scan import selective_scan_into
 
 
@@ -126,15 +127,19 @@ class MambaBlock(nn.Module):
             conv_state, ssm_state
 
     def step_2d(self, x: torch.Tensor, conv_state: torch.Tensor, ssm_state: torch.Tensor,
-                resid: torch.Tensor | None = None):
+                resid: torch.Tensor | None = None, next_norm: nn.Module | None = None):
         """The decode step on a (B, d_model) row block, states updated in place.
 
         in_proj GEMM + conv-window step -> x_proj GEMM -> fused dt_proj + softplus +
         SSM update + C contraction + D skip + SiLU(z) -> out_proj GEMM.  For f16/bf16
         at B <= 64 the GEMMs are the weight-streaming decode kernel with the conv
-        step folded into in_proj and, when ``resid`` is given, the residual add
-        folded into out_proj (the return value is then None: ``resid`` holds
-        x + out_proj(y)).  Otherwise the projections run on torch's GEMM."""
+        step folded into in_proj and, when ``resid`` is given, the residual add (and
+        ``next_norm``, an RMSNorm, when given) folded into out_proj.
+
+        Without ``resid`` returns out_proj(y).  With ``resid`` returns a pair: ``(y,
+        None)`` when the caller still has to add y; ``(None, None)`` when ``resid``
+        already holds x + out_proj(y); ``(None, h)`` when in addition h =
+        next_norm(resid)."""
         di = self.d_inner
         W_in = self.in_proj.weight
         if in_proj_conv_ok(x, W_in, conv_state, self.conv1d.weight, self.conv1d.bias):
@@ -151,9 +156,12 @@ class MambaBlock(nn.Module):
         y = ssm_step_dtproj(ssm_state, x_conv, dt_pre, self.dt_proj.weight, self._A(), Bm, Cm,
                             dt_bias=self.dt_proj.bias, D=self.D, z=z)
         W_out = self.out_proj.weight
-        if decode_linear_ok(y, W_out):
-            if resid is not None and resid.dtype == y.dtype and resid.stride(-1) == 1:
-                decode_linear_resid_(resid, y, W_out)
-                return None
-            return decode_linear(y, W_out)
-        return self.out_proj(y)
+        fused = decode_linear_ok(y, W_out)
+        if resid is None:
+            return decode_linear(y, W_out) if fused else self.out_proj(y)
+        if not (fused and resid.dtype == y.dtype and resid.stride(-1) == 1):
+            return self.out_proj(y), None
+        if next_norm is not None and next_norm.weight.dtype == y.dtype:
+            return None, decode_linear_resid_norm_(resid, y, W_out, next_norm.weight, next_norm.eps)
+        decode_linear_resid_(resid, y, W_out)
+        return None, None

@@ -80,18 +80,21 @@ class MambaModel(nn.Module):
     def _run(self, input_ids, mix):
         """Layer chain with the residual add fused into the next layer's RMSNorm:
         resid += y_prev; h = RMSNorm(resid) (one kernel per layer boundary).
-        ``mix(mixer, h, resid)`` returns the mixer output, or None when it has
-        already added it into ``resid`` itself."""
+        ``mix(mixer, h, resid, next_norm)`` returns either ``(y, None)`` -- the mixer
+        output, added here -- or ``(None, h_next)`` when it has already added its
+        output into ``resid`` and applied ``next_norm`` itself."""
         resid = self.embeddings(input_ids)
-        y = None
-        for layer in self.layers:
-            h = add_rmsnorm(resid, y, layer.norm.weight, layer.norm.eps)
-            y = mix(layer.mixer, h, resid)
-        return add_rmsnorm(resid, y, self.norm_f.weight, self.norm_f.eps)
+        norms = [layer.norm for layer in self.layers] + [self.norm_f]
+        h = add_rmsnorm(resid, None, norms[0].weight, norms[0].eps)
+        for i, layer in enumerate(self.layers):
+            y, h_next = mix(layer.mixer, h, resid, norms[i + 1])
+            h = h_next if h_next is not None else add_rmsnorm(resid, y, norms[i + 1].weight,
+                                                              norms[i + 1].eps)
+        return h
 
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
         """input_ids (B, L) -> logits (B, L, vocab_size)."""
-        return self._head(self._run(input_ids, lambda m, h, resid: m(h)))
+        return self._head(self._run(input_ids, lambda m, h, resid, nrm: (m(h), None)))
 
     def init_state(self, batch_size: int = 1):
         """Zero conv and SSM states (float32, as mamba_model.py:80-91)."""
@@ -109,11 +112,11 @@ class MambaModel(nn.Module):
         conv_states, ssm_states)."""
         convs, ssms = [], []
 
-        def mix(m, h, resid):
+        def mix(m, h, resid, nrm):
             y, cs, ss = m.prefill(h)
             convs.append(cs)
             ssms.append(ss)
-            return y
+            return y, None
 
         h = self._run(input_ids, mix)
         if last_only:
@@ -129,9 +132,9 @@ class MambaModel(nn.Module):
             ssm_states = [t.clone() for t in ssm_states]
         it = iter(zip(conv_states, ssm_states))
 
-        def mix(m, h, resid):
+        def mix(m, h, resid, nrm):
             cs, ss = next(it)
-            return m.step_2d(h, cs, ss, resid=resid)
+            return m.step_2d(h, cs, ss, resid=resid, next_norm=nrm)
 
         h = self._run(input_ids.reshape(-1), mix)
         return self._head(h)[:, None, :], list(conv_states), list(ssm_states)

@@ -108,6 +108,33 @@ def test_decode_linear_resid(dev, dtype):
     assert (err <= bound).all(), f"resid: worst excess {float((err - bound).max()):.3e}"
 
 
+# (64, 5120, 2560): split K, fused reduce + residual + norm pass; (64, 1024, 8192):
+# unsplit, RESID epilogue then the norm kernel; (40, 1024, 1001): split with N % 4 != 0
+# (ordered reduce, then the norm kernel); (1, 1536, 768): 130M out_proj at batch 1.
+@pytest.mark.parametrize("M,K,N", [(64, 5120, 2560), (64, 1024, 8192), (40, 1024, 1001),
+                                   (1, 1536, 768)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_linear_resid_norm(dev, M, K, N, dtype):
+    """resid += round(y @ w.T); out = RMSNorm(resid) * norm_w, against fp32 torch."""
+    from mamba_metal_amd.linear import decode_linear_resid_norm_
+
+    g = torch.Generator(device=dev).manual_seed(M + K + N)
+    y = torch.randn((M, K), generator=g, device=dev).to(dtype)
+    w = (torch.randn((N, K), generator=g, device=dev) * 0.02).to(dtype)
+    resid = torch.randn((M, N), generator=g, device=dev).to(dtype)
+    nw = (1.0 + 0.1 * torch.randn((N,), generator=g, device=dev)).to(dtype)
+    r0 = resid.float().cpu().numpy()
+    yr = _ref(y, w).to(dtype).float().cpu().numpy()
+    out = decode_linear_resid_norm_(resid, y, w, nw, 1e-5)
+    got_r = resid.float().cpu().numpy()
+    err = np.abs(got_r - (r0 + yr))
+    assert (err <= TOL[dtype] * (np.abs(r0) + np.abs(yr)) + 1e-6).all(), "residual"
+    # the norm of the residual the kernel produced (rounded to dtype, as stored)
+    ref = numpy_ref.rms_norm(got_r.astype(np.float64), nw.float().cpu().numpy().astype(np.float64),
+                             eps=1e-5)
+    assert_close(out.float().cpu().numpy(), ref, TOL[dtype], TOL[dtype], f"norm M={M} N={N}")
+
+
 @pytest.mark.parametrize("M", [64, 3])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_decode_in_proj_conv(dev, M, dtype):
