@@ -34,7 +34,20 @@
 namespace mm {
 namespace scan {
 
+#ifndef MM_SCAN_PF
+#define MM_SCAN_PF 1
+#endif
+#ifndef MM_SCAN_G16
+#define MM_SCAN_G16 8
+#endif
+#ifndef MM_SCAN_SPL16
+#define MM_SCAN_SPL16 2
+#endif
+
 constexpr int kCPW = 64;     // channels per workgroup (lanes per wave)
+// Tiles of u/delta/z/B/C loaded ahead of the scan.  Deeper prefetch measured slower
+// on MI355X (the slot-indexed buffers are then moved to LDS by the compiler).
+constexpr int kPF = MM_SCAN_PF;
 constexpr int kT = 32;       // timesteps per tile
 constexpr int kTP = kT + 4;  // padded LDS row length (floats)
 constexpr int kSpinLimit = 1 << 26;
@@ -75,8 +88,8 @@ inline void pick_shape(int64_t dstate, int* groups, int* spl) {
   // 8 waves x 2 states for dstate <= 16 (enough waves per CU to hide the exp and LDS
   // latency at one workgroup per CU); 4 waves x SPL above.
   if (dstate <= 16) {
-    *groups = 8;
-    *spl = dstate <= 8 ? 1 : 2;
+    *groups = MM_SCAN_G16;
+    *spl = dstate <= 8 ? (MM_SCAN_SPL16 > 1 ? MM_SCAN_SPL16 / 2 : 1) : MM_SCAN_SPL16;
   } else {
     *groups = 4;
     *spl = dstate <= 32 ? 8 : 16;
@@ -143,7 +156,7 @@ __device__ __forceinline__ float softplus_log2(float x) {
 }
 
 // ---------------------------------------------------------------------------
-template <int DT, int LAYOUT, int SPL, int G>
+template <int DT, int LAYOUT, int SPL, int G, bool VEC>
 __global__ __launch_bounds__(kCPW * G) void scan_kernel(
     const Params p, const void* __restrict__ u_, const void* __restrict__ delta_,
     const void* __restrict__ z_, void* __restrict__ y_, const float* __restrict__ bc_,
@@ -207,41 +220,49 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
       Dv[j] = (p.D != nullptr && d < p.dim) ? p.D[d * p.Ds] : 0.0f;
     }
 
-    VE ru, rd, rz;
-    float4 rbc[BCPT];
-    auto load_raw = [&](int64_t t0) {
+    VE ru_[kPF], rd_[kPF], rz_[kPF];
+    float4 rbc_[kPF][BCPT];
+    // All loads are unconditional from clamped, in-bounds addresses (elements outside
+    // the tensors read element (b, 0, 0); z, when absent, reads u): the prologue masks
+    // those elements and the epilogue never stores them.  Guarded loads would make
+    // the compiler wait for every outstanding load at the first use, which defeats
+    // the kPF-deep prefetch.
+    const T* const zsrc = static_cast<const T*>(has_z ? z_ : u_);
+    const int64_t zs0 = has_z ? p.zs0 : p.us0, zs1 = has_z ? p.zs1 : p.us1,
+                  zs2 = has_z ? p.zs2 : p.us2;
+    auto load_raw = [&](int slot, int64_t t0) {
+      VE& ru = ru_[slot];
+      VE& rd = rd_[slot];
+      VE& rz = rz_[slot];
+      float4* rbc = rbc_[slot];
 #pragma unroll
       for (int i = 0; i < BCPT; ++i) {
-        const int v = tid + i * NT;
-        if (v < BCV) {
-          const int gg = v / (kT * 2 * SPL / 4), rest = v % (kT * 2 * SPL / 4);
-          rbc[i] = *reinterpret_cast<const float4*>(
-              bc_ + ((b * G + gg) * p.Lp + t0) * (2 * SPL) + rest * 4);
-        }
+        const int v = (tid + i * NT) % BCV;
+        const int gg = v / (kT * 2 * SPL / 4), rest = v % (kT * 2 * SPL / 4);
+        rbc[i] = *reinterpret_cast<const float4*>(
+            bc_ + ((b * G + gg) * p.Lp + t0) * (2 * SPL) + rest * 4);
       }
-      if (p.vec_ok) {
+      if constexpr (VEC) {
         const bool in = (d0 + vc < p.dim) && (t0 + vt < p.seqlen);
-        const int64_t cu = b * p.us0 + (d0 + vc) * p.us1 + (t0 + vt) * p.us2;
-        const int64_t cd = b * p.ds0 + (d0 + vc) * p.ds1 + (t0 + vt) * p.ds2;
-        const int64_t cz = b * p.zs0 + (d0 + vc) * p.zs1 + (t0 + vt) * p.zs2;
-        const VE zero = {};
-        ru = in ? *reinterpret_cast<const VE*>(static_cast<const T*>(u_) + cu) : zero;
-        rd = in ? *reinterpret_cast<const VE*>(static_cast<const T*>(delta_) + cd) : zero;
-        rz = (in && has_z) ? *reinterpret_cast<const VE*>(static_cast<const T*>(z_) + cz) : zero;
+        const int64_t dc = in ? d0 + vc : 0, tc = in ? t0 + vt : 0;
+        ru = *reinterpret_cast<const VE*>(static_cast<const T*>(u_) + b * p.us0 + dc * p.us1 + tc * p.us2);
+        rd = *reinterpret_cast<const VE*>(static_cast<const T*>(delta_) + b * p.ds0 + dc * p.ds1 + tc * p.ds2);
+        rz = *reinterpret_cast<const VE*>(zsrc + b * zs0 + dc * zs1 + tc * zs2);
       } else {
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
-          const int64_t d = d0 + ec(j), t = t0 + et(j);
-          const bool in = d < p.dim && t < p.seqlen;
-          ru[j] = in ? static_cast<const T*>(u_)[b * p.us0 + d * p.us1 + t * p.us2] : T(0);
-          rd[j] = in ? static_cast<const T*>(delta_)[b * p.ds0 + d * p.ds1 + t * p.ds2] : T(0);
-          rz[j] = (in && has_z) ? static_cast<const T*>(z_)[b * p.zs0 + d * p.zs1 + t * p.zs2]
-                                : T(0);
+          const bool in = (d0 + ec(j) < p.dim) && (t0 + et(j) < p.seqlen);
+          const int64_t dc = in ? d0 + ec(j) : 0, tc = in ? t0 + et(j) : 0;
+          ru[j] = static_cast<const T*>(u_)[b * p.us0 + dc * p.us1 + tc * p.us2];
+          rd[j] = static_cast<const T*>(delta_)[b * p.ds0 + dc * p.ds1 + tc * p.ds2];
+          rz[j] = zsrc[b * zs0 + dc * zs1 + tc * zs2];
         }
       }
     };
 
-    load_raw(tile0 * kT);
+#pragma unroll
+    for (int q = 0; q < kPF; ++q)
+      if (tile0 + q < tile1) load_raw(q, (tile0 + q) * kT);
 
     // ---- carried state from the previous segment of this chain ----
     if (seg > 0) {
@@ -263,7 +284,11 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
         h[k] = __hip_atomic_load(cp + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    for (int64_t tile = tile0; tile < tile1; ++tile) {
+    auto process = [&](int slot, int64_t tile) {
+      const VE& ru = ru_[slot];
+      const VE& rd = rd_[slot];
+      const VE& rz = rz_[slot];
+      const float4* rbc = rbc_[slot];
       const int64_t t0 = tile * kT;
       const bool full = (t0 + kT <= p.seqlen) && (d0 + kCPW <= p.dim);
 
@@ -305,7 +330,7 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
         const int v = tid + i * NT;
         if (v < BCV) reinterpret_cast<float4*>(&s_bc[0][0][0])[v] = rbc[i];
       }
-      if (tile + 1 < tile1) load_raw(t0 + kT);  // in flight during the scan
+      if (tile + kPF < tile1) load_raw(slot, t0 + kPF * kT);  // in flight during the scans
       __syncthreads();
 
       // ---- scan: lane = channel, wave = state group; LDS reads one group ahead ----
@@ -355,11 +380,18 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
 #pragma unroll
       for (int j = 0; j < EPT; ++j) yv[j] = yskip[j];
       if (LAYOUT == kTimeContig) {
+        // all G partial reads in flight before the (in-order) sum
+        float4 part[G][EPT / 4];
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+          for (int j = 0; j < EPT; j += 4)
+            part[gg][j / 4] = *reinterpret_cast<const float4*>(&s_y[gg][vc][vt + j]);
 #pragma unroll
         for (int gg = 0; gg < G; ++gg)
 #pragma unroll
           for (int j = 0; j < EPT; j += 4) {
-            const float4 a = *reinterpret_cast<const float4*>(&s_y[gg][vc][vt + j]);
+            const float4 a = part[gg][j / 4];
             yv[j] += a.x; yv[j + 1] += a.y; yv[j + 2] += a.z; yv[j + 3] += a.w;
           }
       } else {
@@ -371,7 +403,7 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
       VE ry;
 #pragma unroll
       for (int j = 0; j < EPT; ++j) ry[j] = Ty<DT>::from(yv[j] * gate[j]);
-      if (p.vec_ok) {
+      if constexpr (VEC) {
         if ((d0 + vc < p.dim) && (t0 + vt < p.seqlen))
           *reinterpret_cast<VE*>(static_cast<T*>(y_) + b * p.ys0 + (d0 + vc) * p.ys1 +
                                  (t0 + vt) * p.ys2) = ry;
@@ -383,6 +415,11 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
             static_cast<T*>(y_)[b * p.ys0 + d * p.ys1 + t * p.ys2] = ry[j];
         }
       }
+    };
+    for (int64_t tile = tile0; tile < tile1; tile += kPF) {
+#pragma unroll
+      for (int q = 0; q < kPF; ++q)
+        if (tile + q < tile1) process(q, tile + q);
     }
 
     // ---- hand the state on, or write the final state ----
@@ -437,9 +474,9 @@ int num_cus() {
   return cached[dev];
 }
 
-template <int DT, int LAYOUT, int SPL, int G>
-void launch(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w) {
-  auto kern = scan_kernel<DT, LAYOUT, SPL, G>;
+template <int DT, int LAYOUT, int SPL, int G, bool VEC>
+void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w) {
+  auto kern = scan_kernel<DT, LAYOUT, SPL, G, VEC>;
   char* ws = static_cast<char*>(a->workspace);
   int* ctl = reinterpret_cast<int*>(ws);
   float* carry = reinterpret_cast<float*>(ws + w.carry);
@@ -451,13 +488,29 @@ void launch(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w)
                      a->delta, a->z, a->y, bc, a->state_out, ctl, carry);
 }
 
+template <int DT, int LAYOUT, int SPL, int G>
+void launch(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w) {
+  if (p.vec_ok) launch_k<DT, LAYOUT, SPL, G, true>(p, a, s, w);
+  else launch_k<DT, LAYOUT, SPL, G, false>(p, a, s, w);
+}
+
+// The (SPL, G) instantiation must be exactly the shape the workspace was laid out
+// for (ws_layout sizes the B/C pack and the carries by groups * spl): every shape
+// pick_shape can return has its own case, and anything else is an error.
+inline bool shape_known(int groups, int spl) {
+  return (groups == 8 && (spl == 1 || spl == 2)) ||
+         (groups == 4 && (spl == 2 || spl == 4 || spl == 8 || spl == 16));
+}
+
 template <int DT, int LAYOUT>
 void launch_shape(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w, int groups,
                   int spl) {
   if (groups == 8 && spl == 1) launch<DT, LAYOUT, 1, 8>(p, a, s, w);
-  else if (groups == 8) launch<DT, LAYOUT, 2, 8>(p, a, s, w);
-  else if (spl == 8) launch<DT, LAYOUT, 8, 4>(p, a, s, w);
-  else launch<DT, LAYOUT, 16, 4>(p, a, s, w);
+  else if (groups == 8 && spl == 2) launch<DT, LAYOUT, 2, 8>(p, a, s, w);
+  else if (groups == 4 && spl == 2) launch<DT, LAYOUT, 2, 4>(p, a, s, w);
+  else if (groups == 4 && spl == 4) launch<DT, LAYOUT, 4, 4>(p, a, s, w);
+  else if (groups == 4 && spl == 8) launch<DT, LAYOUT, 8, 4>(p, a, s, w);
+  else if (groups == 4 && spl == 16) launch<DT, LAYOUT, 16, 4>(p, a, s, w);
 }
 
 template <int DT>
@@ -483,9 +536,11 @@ void launch_pack(const mm_scan_params* a, int64_t Lp, int groups, int spl, const
                      a->B_stride[0], a->B_stride[1], a->B_stride[2], a->C_stride[0],             \
                      a->C_stride[1], a->C_stride[2])
   if (groups == 8 && spl == 1) MM_PACK(1, 8);
-  else if (groups == 8) MM_PACK(2, 8);
-  else if (spl == 8) MM_PACK(8, 4);
-  else MM_PACK(16, 4);
+  else if (groups == 8 && spl == 2) MM_PACK(2, 8);
+  else if (groups == 4 && spl == 2) MM_PACK(2, 4);
+  else if (groups == 4 && spl == 4) MM_PACK(4, 4);
+  else if (groups == 4 && spl == 8) MM_PACK(8, 4);
+  else if (groups == 4 && spl == 16) MM_PACK(16, 4);
 #undef MM_PACK
 }
 
@@ -557,6 +612,8 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
 
   int groups = 8, spl = 2;
   pick_shape(a->dstate, &groups, &spl);
+  if (!shape_known(groups, spl))
+    return fail(MM_ERR_DSTATE, "no scan instantiation for %d groups x %d states", groups, spl);
   const int ept = kCPW * kT / (kCPW * groups);
   int layout = kTimeContig, vec_ok = 0;
   choose_layout(a, ept, &layout, &vec_ok);
