@@ -171,9 +171,17 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
   constexpr int BCV = BCF / 4;
   constexpr int BCPT = (BCV + NT - 1) / NT;
 
-  __shared__ __attribute__((aligned(16))) float s_dt[kCPW][kTP];    // delta2
-  __shared__ __attribute__((aligned(16))) float s_du[kCPW][kTP];    // delta2 * u
-  __shared__ __attribute__((aligned(16))) float s_y[G][kCPW][kTP];  // partial y
+  // LDS tiles of delta2, delta2*u and the G partial y's.  Time-contiguous inputs stage
+  // them channel-major ([channel][time], rows of kTP floats); channel-contiguous
+  // inputs time-major ([time][channel], rows of kCP floats), so that the prologue's
+  // and the epilogue's float4 accesses run along the axis each thread owns and hit
+  // distinct banks either way.
+  constexpr int kCP = kCPW + 4;
+  constexpr int TILE_F = (LAYOUT == kTimeContig) ? kCPW * kTP : kT * kCP;
+  __shared__ __attribute__((aligned(16))) float s_dt[TILE_F];
+  __shared__ __attribute__((aligned(16))) float s_du[TILE_F];
+  __shared__ __attribute__((aligned(16))) float s_y[G][TILE_F];
+  auto at = [](int c, int t) { return (LAYOUT == kTimeContig) ? c * kTP + t : t * kCP + c; };
   __shared__ __attribute__((aligned(16))) float s_bc[G][kT][2 * SPL];
   __shared__ int s_ticket;
 
@@ -182,9 +190,12 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
   const int g = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool has_z = z_ != nullptr;
 
-  // Element ownership for prologue/epilogue.
-  const int vc = (LAYOUT == kTimeContig) ? (tid / TPC) : ((tid / kT) * EPT);
-  const int vt = (LAYOUT == kTimeContig) ? ((tid % TPC) * EPT) : (tid % kT);
+  // Element ownership for the prologue / epilogue: consecutive threads walk the
+  // contiguous axis, so a wave's vector access covers whole 128-byte rows -- along
+  // time (TPC threads per channel row) or along channels (CPT threads per step row).
+  constexpr int CPT = kCPW / EPT;
+  const int vc = (LAYOUT == kTimeContig) ? (tid / TPC) : ((tid % CPT) * EPT);
+  const int vt = (LAYOUT == kTimeContig) ? ((tid % TPC) * EPT) : (tid / CPT);
   auto ec = [&](int j) { return (LAYOUT == kTimeContig) ? vc : vc + j; };
   auto et = [&](int j) { return (LAYOUT == kTimeContig) ? vt + j : vt; };
 
@@ -315,14 +326,14 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
       if (LAYOUT == kTimeContig) {
 #pragma unroll
         for (int j = 0; j < EPT; j += 4) {
-          *reinterpret_cast<float4*>(&s_dt[vc][vt + j]) = make_float4(dtv[j], dtv[j + 1], dtv[j + 2], dtv[j + 3]);
-          *reinterpret_cast<float4*>(&s_du[vc][vt + j]) = make_float4(duv[j], duv[j + 1], duv[j + 2], duv[j + 3]);
+          *reinterpret_cast<float4*>(&s_dt[at(vc, vt + j)]) = make_float4(dtv[j], dtv[j + 1], dtv[j + 2], dtv[j + 3]);
+          *reinterpret_cast<float4*>(&s_du[at(vc, vt + j)]) = make_float4(duv[j], duv[j + 1], duv[j + 2], duv[j + 3]);
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < EPT; ++j) {
-          s_dt[vc + j][vt] = dtv[j];
-          s_du[vc + j][vt] = duv[j];
+        for (int j = 0; j < EPT; j += 4) {
+          *reinterpret_cast<float4*>(&s_dt[at(vc + j, vt)]) = make_float4(dtv[j], dtv[j + 1], dtv[j + 2], dtv[j + 3]);
+          *reinterpret_cast<float4*>(&s_du[at(vc + j, vt)]) = make_float4(duv[j], duv[j + 1], duv[j + 2], duv[j + 3]);
         }
       }
 #pragma unroll
@@ -339,8 +350,15 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
         float bc[4][2 * SPL];
       };
       auto fetch = [&](int tt, Grp& gr) {
-        gr.d4 = *reinterpret_cast<const float4*>(&s_dt[lane][tt]);
-        gr.u4 = *reinterpret_cast<const float4*>(&s_du[lane][tt]);
+        if constexpr (LAYOUT == kTimeContig) {
+          gr.d4 = *reinterpret_cast<const float4*>(&s_dt[at(lane, tt)]);
+          gr.u4 = *reinterpret_cast<const float4*>(&s_du[at(lane, tt)]);
+        } else {
+          gr.d4 = make_float4(s_dt[at(lane, tt)], s_dt[at(lane, tt + 1)], s_dt[at(lane, tt + 2)],
+                              s_dt[at(lane, tt + 3)]);
+          gr.u4 = make_float4(s_du[at(lane, tt)], s_du[at(lane, tt + 1)], s_du[at(lane, tt + 2)],
+                              s_du[at(lane, tt + 3)]);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -371,7 +389,12 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
           }
           ys[j] = acc;
         }
-        *reinterpret_cast<float4*>(&s_y[g][lane][tt]) = make_float4(ys[0], ys[1], ys[2], ys[3]);
+        if constexpr (LAYOUT == kTimeContig) {
+          *reinterpret_cast<float4*>(&s_y[g][at(lane, tt)]) = make_float4(ys[0], ys[1], ys[2], ys[3]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) s_y[g][at(lane, tt + j)] = ys[j];
+        }
       }
       __syncthreads();
 
@@ -386,7 +409,7 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
         for (int gg = 0; gg < G; ++gg)
 #pragma unroll
           for (int j = 0; j < EPT; j += 4)
-            part[gg][j / 4] = *reinterpret_cast<const float4*>(&s_y[gg][vc][vt + j]);
+            part[gg][j / 4] = *reinterpret_cast<const float4*>(&s_y[gg][at(vc, vt + j)]);
 #pragma unroll
         for (int gg = 0; gg < G; ++gg)
 #pragma unroll
@@ -395,10 +418,19 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
             yv[j] += a.x; yv[j + 1] += a.y; yv[j + 2] += a.z; yv[j + 3] += a.w;
           }
       } else {
+        float4 part[G][EPT / 4];
 #pragma unroll
-        for (int j = 0; j < EPT; ++j)
+        for (int gg = 0; gg < G; ++gg)
 #pragma unroll
-          for (int gg = 0; gg < G; ++gg) yv[j] += s_y[gg][vc + j][vt];
+          for (int j = 0; j < EPT; j += 4)
+            part[gg][j / 4] = *reinterpret_cast<const float4*>(&s_y[gg][at(vc + j, vt)]);
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+          for (int j = 0; j < EPT; j += 4) {
+            const float4 a = part[gg][j / 4];
+            yv[j] += a.x; yv[j + 1] += a.y; yv[j + 2] += a.z; yv[j + 3] += a.w;
+          }
       }
       VE ry;
 #pragma unroll
