@@ -116,8 +116,9 @@ def copy_probe_gbs():
     return 2 * n * 2 / (ms * 1e-3) / 1e9
 
 
-def cpu_baseline(batch, dim, dstate, seqlen, n_channels=1024):
-    """C oracle (fp32 math, OpenMP) on n_channels of the workload, scaled to all B*D."""
+def cpu_baseline(batch, dim, dstate, seqlen, n_channels=5120):
+    """C oracle (fp32 math, OpenMP) on n_channels of the workload -- a quarter of
+    config 4, about 12 s of CPU work on 16 threads -- scaled to all B*D."""
     import numpy as np
 
     from oracle import cscan
@@ -141,7 +142,7 @@ def cpu_baseline(batch, dim, dstate, seqlen, n_channels=1024):
             "kind": "port",
             "sample": f"{batch * per_b} of {batch * dim} channels ({per_b} per batch row), "
                       f"L={seqlen}, N={dstate}, fp16-rounded inputs, D+z+softplus+state; "
-                      f"{dt:.2f} s measured, scaled x{scale:.0f}",
+                      f"{dt:.2f} s wall on {cscan.num_threads()} threads measured, scaled x{scale:.0f}",
             "sample_seconds": dt}
 
 
