@@ -259,6 +259,14 @@ size_t mm_decode_linear_workspace_size(int64_t M, int64_t N, int64_t K);
 int mm_decode_linear(const mm_linear_params* params, void* stream);
 
 /* ------------------------------------------------------------------------- */
+/* Greedy token choice -- replaces `mx.argmax(logits[:, -1, :], axis=-1)` of
+ * generate_fast (generate.py:91-93): out[r] = index of the largest x[r, 0:n]
+ * (lowest index on ties, a NaN beats every number).  x rows of stride >= n in
+ * dtype; out int64 (rows,). */
+int mm_argmax_rows(const void* x, int64_t rows, int64_t n, int64_t stride, int32_t dtype,
+                   int64_t* out, void* stream);
+
+/* ------------------------------------------------------------------------- */
 /* Pair-scan primitive -- replaces mamba_metal/kernels/pair_scan.metal:1-76
  * (dispatched by experiments/05-pair-scan/pair_scan.py:23-33), without its
  * n <= 1024 limit: inclusive scan of (a, b) under (a2,b2)o(a1,b1) =

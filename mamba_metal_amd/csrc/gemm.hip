@@ -85,16 +85,19 @@ struct Plan {
 };
 
 // Launch shape (from a sweep on MI355X over the decode shapes of Mamba-130M..2.8B):
-// NT = 2 n-tiles per wave once N has >= 256 32-column tiles.  With >= 128 column
-// tiles K stays in the workgroup, with up to 4 waves splitting it; below that, K is
-// split over single-wave workgroups until ~640 of them fill the chip, each keeping
+// NT = 2 n-tiles per wave once N has >= 256 32-column tiles.  K stays in the
+// workgroup (up to 4 waves splitting it) when there are >= 128 column tiles or when
+// one workgroup's share of W is small (<= 160 KB: a second kernel for a split-K
+// reduction costs more than it saves, which is the batch-1 decode case); otherwise K
+// is split over single-wave workgroups until ~640 of them fill the chip, each keeping
 // >= 2 chunks of K.
 inline Plan plan(int64_t N, int64_t K) {
   const int64_t nchunks = K / kChunkK;
   Plan p{1, 1, 1};
   if (ceil_div(N, kTileN) >= 256) p.nt = 2;
   const int64_t ntiles = ceil_div(N, kTileN * p.nt);
-  if (ntiles >= 128) {
+  const int64_t wg_bytes = kTileN * p.nt * K * 2;
+  if (ntiles >= 128 || wg_bytes <= (160 << 10)) {
     while (p.ksw < 4 && ntiles * p.ksw < 512 && nchunks / (p.ksw * 2) >= 2) p.ksw *= 2;
   } else {
     while (p.ks < 64 && ntiles * p.ks < 640 && nchunks / (p.ks * 2) >= 2) p.ks *= 2;

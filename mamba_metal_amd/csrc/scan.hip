@@ -45,9 +45,9 @@ namespace scan {
 #endif
 
 constexpr int kCPW = 64;     // channels per workgroup (lanes per wave)
-// Tiles of u/delta/z/B/C loaded ahead of the scan.  Deeper prefetch measured slower
-// on MI355X (the slot-indexed buffers are then moved to LDS by the compiler).
+// Tiles of u/delta/z/B/C loaded ahead of the scan (1 or 2).
 constexpr int kPF = MM_SCAN_PF;
+static_assert(kPF == 1 || kPF == 2, "prefetch depth");
 constexpr int kT = 32;       // timesteps per tile
 constexpr int kTP = kT + 4;  // padded LDS row length (floats)
 constexpr int kSpinLimit = 1 << 26;
@@ -231,8 +231,10 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
       Dv[j] = (p.D != nullptr && d < p.dim) ? p.D[d * p.Ds] : 0.0f;
     }
 
-    VE ru_[kPF], rd_[kPF], rz_[kPF];
-    float4 rbc_[kPF][BCPT];
+    // Prefetch slots: named variables passed by reference to always-inlined lambdas, so
+    // they stay in registers (an array indexed by slot would be moved to LDS).
+    VE ru0, rd0, rz0, ru1, rd1, rz1;
+    float4 rbc0[BCPT], rbc1[BCPT];
     // All loads are unconditional from clamped, in-bounds addresses (elements outside
     // the tensors read element (b, 0, 0); z, when absent, reads u): the prologue masks
     // those elements and the epilogue never stores them.  Guarded loads would make
@@ -241,11 +243,8 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
     const T* const zsrc = static_cast<const T*>(has_z ? z_ : u_);
     const int64_t zs0 = has_z ? p.zs0 : p.us0, zs1 = has_z ? p.zs1 : p.us1,
                   zs2 = has_z ? p.zs2 : p.us2;
-    auto load_raw = [&](int slot, int64_t t0) {
-      VE& ru = ru_[slot];
-      VE& rd = rd_[slot];
-      VE& rz = rz_[slot];
-      float4* rbc = rbc_[slot];
+    auto load_raw = [&](VE& ru, VE& rd, VE& rz, float4 (&rbc)[BCPT], int64_t t0)
+                        __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < BCPT; ++i) {
         const int v = (tid + i * NT) % BCV;
@@ -271,9 +270,8 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
       }
     };
 
-#pragma unroll
-    for (int q = 0; q < kPF; ++q)
-      if (tile0 + q < tile1) load_raw(q, (tile0 + q) * kT);
+    load_raw(ru0, rd0, rz0, rbc0, tile0 * kT);
+    if (kPF > 1 && tile0 + 1 < tile1) load_raw(ru1, rd1, rz1, rbc1, (tile0 + 1) * kT);
 
     // ---- carried state from the previous segment of this chain ----
     if (seg > 0) {
@@ -295,11 +293,8 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
         h[k] = __hip_atomic_load(cp + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    auto process = [&](int slot, int64_t tile) {
-      const VE& ru = ru_[slot];
-      const VE& rd = rd_[slot];
-      const VE& rz = rz_[slot];
-      const float4* rbc = rbc_[slot];
+    auto process = [&](VE& ru, VE& rd, VE& rz, float4 (&rbc)[BCPT], int64_t tile)
+                       __attribute__((always_inline)) {
       const int64_t t0 = tile * kT;
       const bool full = (t0 + kT <= p.seqlen) && (d0 + kCPW <= p.dim);
 
@@ -341,7 +336,7 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
         const int v = tid + i * NT;
         if (v < BCV) reinterpret_cast<float4*>(&s_bc[0][0][0])[v] = rbc[i];
       }
-      if (tile + kPF < tile1) load_raw(slot, t0 + kPF * kT);  // in flight during the scans
+      if (tile + kPF < tile1) load_raw(ru, rd, rz, rbc, t0 + kPF * kT);  // in flight during the scans
       __syncthreads();
 
       // ---- scan: lane = channel, wave = state group; LDS reads one group ahead ----
@@ -449,9 +444,8 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
       }
     };
     for (int64_t tile = tile0; tile < tile1; tile += kPF) {
-#pragma unroll
-      for (int q = 0; q < kPF; ++q)
-        if (tile + q < tile1) process(q, tile + q);
+      process(ru0, rd0, rz0, rbc0, tile);
+      if (kPF > 1 && tile + 1 < tile1) process(ru1, rd1, rz1, rbc1, tile + 1);
     }
 
     // ---- hand the state on, or write the final state ----

@@ -20,10 +20,19 @@ from typing import Callable
 
 import torch
 
+from mamba_metal_amd.sample import argmax_rows
+
+
+def _argmax(logits: torch.Tensor) -> torch.Tensor:
+    """Greedy ids over the last axis on the library kernel (rows flattened)."""
+    flat = logits.reshape(-1, logits.shape[-1]) if logits.stride(-1) == 1 else \
+        logits.contiguous().reshape(-1, logits.shape[-1])
+    return argmax_rows(flat).reshape(logits.shape[:-1])
+
 
 def _sample(logits: torch.Tensor, temperature: float, generator=None) -> torch.Tensor:
     if temperature == 0.0:
-        return torch.argmax(logits, dim=-1)
+        return _argmax(logits)
     probs = torch.softmax(logits.float() / temperature, dim=-1)
     return torch.multinomial(probs, 1, generator=generator).squeeze(-1)
 
@@ -112,13 +121,13 @@ class GraphDecoder:
 
     def _eager_step(self):
         logits, _, _ = self.model.step(self.ids.view(-1, 1), self.convs, self.ssms)
-        return torch.argmax(logits[:, 0, :], dim=-1)
+        return _argmax(logits[:, 0, :])
 
     @torch.inference_mode()
     def start(self, input_ids: torch.Tensor) -> torch.Tensor:
         assert input_ids.shape[0] == self.batch
         logits, convs, ssms = self.model.prefill(input_ids, last_only=True)
-        first = torch.argmax(logits[:, -1, :], dim=-1)
+        first = _argmax(logits[:, -1, :])
         if self.convs is None:
             self.convs, self.ssms = convs, ssms
             self.ids = first.clone()

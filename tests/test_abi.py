@@ -204,6 +204,15 @@ def test_decode_linear_validation(lib):
     assert lib.mm_pack_linear_weight(FAKE, FAKE, 50, 64, 64, _lib.F32, None) == _lib.ERR_DTYPE
 
 
+def test_argmax_validation(lib):
+    out = FAKE
+    assert lib.mm_argmax_rows(None, 2, 8, 8, _lib.F16, out, None) == _lib.ERR_NULL_POINTER
+    assert lib.mm_argmax_rows(FAKE, 2, 0, 8, _lib.F16, out, None) == _lib.ERR_SHAPE
+    assert lib.mm_argmax_rows(FAKE, 2, 16, 8, _lib.F16, out, None) == _lib.ERR_LAYOUT
+    assert lib.mm_argmax_rows(FAKE, 2, 8, 8, 9, out, None) == _lib.ERR_DTYPE
+    assert lib.mm_argmax_rows(FAKE, 0, 8, 8, _lib.F16, out, None) == _lib.OK
+
+
 def test_zero_sizes_are_noops(lib):
     # Nothing to do -> MM_OK without touching the (fake) pointers or the device.
     assert _scan(lib, batch=0) == _lib.OK

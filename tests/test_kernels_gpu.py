@@ -254,3 +254,24 @@ def test_add_rmsnorm(dev, dim, dtype):
     assert_close(out.float().cpu().numpy(), ref, rt, at, f"rmsnorm dim={dim}")
     out2 = add_rmsnorm(xt, None, wt, 1e-5)           # no add: plain RMSNorm
     assert_close(out2.float().cpu().numpy(), ref, rt, at, "rmsnorm no-add")
+
+
+@pytest.mark.parametrize("n", [50280, 50277, 768, 1])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_argmax_rows(dev, n, dtype):
+    """Greedy ids == torch.argmax, incl. planted ties (lowest index wins) and NaN."""
+    from mamba_metal_amd.sample import argmax_rows
+
+    g = torch.Generator(device=dev).manual_seed(n)
+    x = torch.randn((37, n), generator=g, device=dev).to(dtype)
+    if n > 10:
+        x[3, 5] = x[3, n - 2] = 100.0            # tie: index 5 wins
+        x[4, 7] = float("nan")                   # NaN beats numbers
+        x[5, :] = 1.0                            # all equal: index 0
+        x[6, :] = float("-inf")                  # all -inf: index 0
+        x[7, 9:] = float("nan")                  # many NaNs: the first one
+    got = argmax_rows(x)
+    assert torch.equal(got, torch.argmax(x, dim=-1))
+    # strided rows (a column slice of a wider buffer)
+    wide = torch.randn((9, n + 24), generator=g, device=dev).to(dtype)
+    assert torch.equal(argmax_rows(wide[:, :n]), torch.argmax(wide[:, :n], dim=-1))

@@ -28,9 +28,12 @@ def _check(got, ref, dtype, what):
 
 # decode shapes of Mamba-2.8B (in/out/x projections, head) and 130M, ragged M/N,
 # split-K (narrow N) and single-chunk K
+# (37, 4096, 100) and (64, 5120, 192) split K over the grid with ragged / narrow N; the
+# 130M batch-1 shapes and the small ones keep K in the workgroup
 @pytest.mark.parametrize("M,K,N", [(64, 2560, 10240), (64, 5120, 2560), (64, 5120, 192),
                                    (1, 768, 3072), (1, 1536, 80), (37, 1536, 100), (33, 256, 50),
-                                   (32, 64, 33), (64, 2560, 50280), (5, 64, 7), (64, 64, 4096)])
+                                   (37, 4096, 100), (32, 64, 33), (64, 2560, 50280), (5, 64, 7),
+                                   (64, 64, 4096)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_decode_linear(dev, M, K, N, dtype):
     from mamba_metal_amd.linear import decode_linear
@@ -55,7 +58,7 @@ def test_decode_linear_split_sequence(dev):
     from mamba_metal_amd.linear import decode_linear
 
     g = torch.Generator(device=dev).manual_seed(11)
-    for (M, K, N) in [(64, 5120, 192), (1, 768, 3072), (64, 5120, 192), (33, 1536, 2000)]:
+    for (M, K, N) in [(64, 5120, 192), (37, 4096, 100), (64, 5120, 192), (33, 5120, 2000)]:
         x = torch.randn((M, K), generator=g, device=dev).half()
         w = (torch.randn((N, K), generator=g, device=dev) * 0.05).half()
         _check(decode_linear(x, w), _ref(x, w), torch.float16, f"sequence M={M} K={K} N={N}")
@@ -109,9 +112,9 @@ def test_decode_linear_resid(dev, dtype):
 
 
 # (64, 5120, 2560): split K, fused reduce + residual + norm pass; (64, 1024, 8192):
-# unsplit, RESID epilogue then the norm kernel; (40, 1024, 1001): split with N % 4 != 0
-# (ordered reduce, then the norm kernel); (1, 1536, 768): 130M out_proj at batch 1.
-@pytest.mark.parametrize("M,K,N", [(64, 5120, 2560), (64, 1024, 8192), (40, 1024, 1001),
+# unsplit, RESID epilogue then the norm kernel; (40, 4096, 1001): split with N % 4 != 0
+# (ordered reduce, then the norm kernel); (1, 1536, 768): 130M out_proj at batch 1 (unsplit).
+@pytest.mark.parametrize("M,K,N", [(64, 5120, 2560), (64, 1024, 8192), (40, 4096, 1001),
                                    (1, 1536, 768)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_decode_linear_resid_norm(dev, M, K, N, dtype):
