@@ -12,18 +12,24 @@
 // elements W[32t + l%32, 16s + 8(l/32) .. +7].  A wave's W load for one MFMA step
 // is then one 1 KB contiguous read -- the access pattern of a plain stream.
 //
-// X goes through LDS: each wave loads its 64-row x 64-k chunk of X with 128-byte
-// row segments (8 rows per load instruction), writes it to a wave-private LDS tile
-// (rows padded to 144 bytes) and reads its A operands from there.
+// X goes through LDS: 64-row x 64-k chunks of X are loaded with 128-byte row
+// segments (8 rows per load instruction), written to an LDS tile (rows padded to 144
+// bytes) and the MFMA A operands are read from there.
 //
-// Work split.  A workgroup owns NT x 32 output columns (NT = 2 for wide N, so each
-// X operand feeds two MFMAs).  Wide calls keep all of K in the workgroup: its KSW
-// waves split K, their partial tiles meet in LDS (summed in fixed wave order) and
-// the epilogue runs in the same kernel.  Narrow calls (too few column tiles to fill
-// the chip) split K over the grid's y dimension instead: single-wave workgroups
-// write fp32 partial tiles, row-major [split][M][N], to the workspace, and a second
-// kernel sums the splits in order and runs the epilogue -- deterministic, and the
-// kernel boundary orders the partials without any cross-workgroup protocol.
+// Work split.  X is as large as 64 columns of W (M = 64), and every workgroup that
+// covers a K range re-reads that range of X from L2; measured on MI355X that traffic
+// costs about as much as the weight stream itself, so the split is chosen to share it:
+//   * very wide N (> 512 column tiles): share_kernel -- NW waves own NW adjacent
+//     32-column tiles, walk all of K together and share one X chunk per step through LDS;
+//   * otherwise linear_kernel, NT 32-column tiles per workgroup (NT = 2 from 256 tiles
+//     on): with enough tiles (or a small weight share) K stays in the workgroup, its KSW
+//     waves split K and their partial tiles meet in LDS (summed in fixed wave order)
+//     before the epilogue.
+//     Narrow calls split K over the grid's y dimension instead: single-wave
+//     workgroups write fp32 partial tiles, row-major [split][M][N], to the workspace,
+//     and a second kernel sums the splits in order and runs the epilogue --
+//     deterministic, and the kernel boundary orders the partials without any
+//     cross-workgroup protocol.
 //
 // Epilogues fold the decode step's neighbouring element-wise ops into the GEMM:
 //   MM_LIN_STORE  y[m, n] = acc
@@ -82,19 +88,29 @@ struct LinParams {
 
 struct Plan {
   int nt, ks, ksw;
+  int nw;  // > 0: shared-X kernel with nw waves splitting N (nt = ks = ksw = 1)
 };
 
-// Launch shape (from a sweep on MI355X over the decode shapes of Mamba-130M..2.8B):
-// NT = 2 n-tiles per wave once N has >= 256 32-column tiles.  K stays in the
-// workgroup (up to 4 waves splitting it) when there are >= 128 column tiles or when
-// one workgroup's share of W is small (<= 160 KB: a second kernel for a split-K
-// reduction costs more than it saves, which is the batch-1 decode case); otherwise K
-// is split over single-wave workgroups until ~640 of them fill the chip, each keeping
-// >= 2 chunks of K.
+// Launch shape (from sweeps on MI355X over the decode shapes of Mamba-130M..2.8B).
+// Very wide N (> 512 32-column tiles: the LM head) runs the shared-X kernel: NW waves
+// split the workgroup's NW x 32 columns, walk all of K together and stage each X chunk
+// in LDS once for all of them, a quarter (NW = 4) or an eighth (NW = 8) of the X
+// traffic per weight byte; NW keeps the grid within 256 workgroups.  For 256..512
+// tiles (in_proj of the large models) a wave owns NT = 2 tiles, so each X operand
+// feeds two MFMAs.  K stays in the workgroup (up to 4 waves splitting it) when there
+// are >= 128 workgroups' worth of column tiles or when one workgroup's share of W is
+// small (<= 160 KB: a second kernel for a split-K reduction costs more than it saves,
+// which is the batch-1 decode case); otherwise K is split over single-wave workgroups
+// until ~640 of them fill the chip, each keeping >= 2 chunks of K.
 inline Plan plan(int64_t N, int64_t K) {
   const int64_t nchunks = K / kChunkK;
-  Plan p{1, 1, 1};
-  if (ceil_div(N, kTileN) >= 256) p.nt = 2;
+  Plan p{1, 1, 1, 0};
+  const int64_t nt32 = ceil_div(N, kTileN);
+  if (nt32 > 512) {
+    p.nw = nt32 <= 1024 ? 4 : 8;
+    return p;
+  }
+  if (nt32 >= 256) p.nt = 2;
   const int64_t ntiles = ceil_div(N, kTileN * p.nt);
   const int64_t wg_bytes = kTileN * p.nt * K * 2;
   if (ntiles >= 128 || wg_bytes <= (160 << 10)) {
@@ -339,6 +355,177 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
   }
 }
 
+// Shared-X kernel for wide N.  Workgroup = NW waves; wave w owns the 32 columns
+// n0 = (blockIdx.x * NW + w) * 32 and all of K.  Per 64-k chunk the waves load the
+// X chunk together (8 rows per load instruction, instruction q by wave q % NW), write
+// it to one of three LDS buffers and meet at a barrier; each wave then runs its 4 x MT
+// MFMAs from that buffer.  W and X loads run two chunks ahead of the MFMAs through a
+// three-slot register ring (named slots: an array indexed by slot would be moved to
+// scratch or LDS).  A buffer is rewritten three chunks after it was read, i.e. after
+// two more barriers, by which time every wave's reads of it have completed.  The
+// epilogue stores straight from the accumulators: lane l holds column n0 + l % 32.
+template <int XPW>
+struct ShareSlot {
+  u32x4 w[kSteps];
+  u32x4 x[XPW];
+};
+
+template <int DT, int NW, int MT, int EPI>
+__global__ __launch_bounds__(NW * 64, 1) void share_kernel(const LinParams p) {
+  using T = typename Ty<DT>::T;
+  constexpr int XQ = MT * 4;                  // X load instructions per chunk (8 rows each)
+  constexpr int XPW = (XQ + NW - 1) / NW;     // per wave
+  constexpr int kBuf = MT * 32 * kRowBytes;
+  __shared__ __align__(16) char xs[3][kBuf];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * NW + wave) * kTileN;
+  const int64_t nsteps = p.K / kStepK;
+  const int64_t nchunks = p.K / kChunkK;
+  const int64_t ntiles32 = (p.N + kTileN - 1) / kTileN;
+  const int64_t tile = n0 / kTileN < ntiles32 ? n0 / kTileN : 0;
+  const u32x4* const wp = static_cast<const u32x4*>(p.w) + tile * nsteps * 64 + lane;
+  // X instruction q = wave + i * NW covers rows 8q .. 8q + 7 (lane: row 8q + l/8,
+  // 16-byte column l % 8).  Slots past XQ re-load a valid row and are not stored.
+  const T* xrow[XPW];
+  bool xok[XPW];
+#pragma unroll
+  for (int i = 0; i < XPW; ++i) {
+    const int q = wave + i * NW;
+    xok[i] = q < XQ;
+    const int64_t r = 8 * (q < XQ ? q : 0) + (lane >> 3);
+    xrow[i] = static_cast<const T*>(p.x) + (r < p.M ? r : 0) * p.ldx + 8 * (lane & 7);
+  }
+  const int rd_off = (lane & 31) * kRowBytes + (lane >> 5) * 16;
+
+  // The conv epilogue's inputs do not depend on the product: load them before the
+  // K loop so their latency hides under it (clamped: lanes past n_conv read column 0).
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  const int64_t n = n0 + (lane & 31);
+  const bool ncol = n < p.N;
+  T4 win[EPI == MM_LIN_CONV ? MT : 1][16];
+  T4 cw{};
+  float bias = 0.0f;
+  if constexpr (EPI == MM_LIN_CONV) {
+    const int64_t nc = n < p.n_conv ? n : 0;
+    const T4* const sb = static_cast<const T4*>(p.conv_state);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t m = 32 * mt + acc_row(i, lane);
+        win[mt][i] = sb[(m < p.M ? m : 0) * p.n_conv + nc];
+      }
+    cw = static_cast<const T4*>(p.conv_w)[nc];
+    const T* const bb = static_cast<const T*>(p.conv_b ? p.conv_b : p.conv_w);
+    bias = p.conv_b ? Ty<DT>::f(bb[nc]) : 0.0f;
+  }
+
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[mt][i] = 0.0f;
+
+  using S = ShareSlot<XPW>;
+  const int64_t clast = nchunks - 1;
+  auto load = [&](S& s, int64_t c) __attribute__((always_inline)) {
+    const int64_t cc = c < nchunks ? c : clast;
+#pragma unroll
+    for (int g = 0; g < kSteps; ++g) s.w[g] = wp[(cc * kSteps + g) * 64];
+#pragma unroll
+    for (int i = 0; i < XPW; ++i) s.x[i] = *reinterpret_cast<const u32x4*>(xrow[i] + cc * kChunkK);
+  };
+  auto compute = [&](S& s, int64_t c, int buf) __attribute__((always_inline)) {
+    if (c >= nchunks) return;  // uniform over the workgroup
+    char* const xb = xs[buf];
+#pragma unroll
+    for (int i = 0; i < XPW; ++i)
+      if (XQ % NW == 0 || xok[i])
+        *reinterpret_cast<u32x4*>(xb + (8 * (wave + i * NW) + (lane >> 3)) * kRowBytes + (lane & 7) * 16) = s.x[i];
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < kSteps; ++g)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(xb + mt * 32 * kRowBytes + rd_off + g * 32);
+        acc[mt] = mfma<DT>(a, s.w[g], acc[mt]);
+      }
+  };
+  S s0, s1, s2;
+  load(s0, 0);
+  load(s1, 1);
+  for (int64_t c = 0; c < nchunks; c += 3) {
+    load(s2, c + 2);
+    compute(s0, c, 0);
+    load(s0, c + 3);
+    compute(s1, c + 1, 1);
+    load(s1, c + 4);
+    compute(s2, c + 2, 2);
+  }
+
+  // ---- epilogue: lane holds column n0 + l % 32, rows 32 mt + acc_row(i, l) ----
+  if constexpr (EPI == MM_LIN_STORE) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t m = 32 * mt + acc_row(i, lane);
+        if (ncol && m < p.M) st<DT>(p.y, m * p.ldy + n, acc[mt][i]);
+      }
+  } else if constexpr (EPI == MM_LIN_RESID) {
+    T* const rb = static_cast<T*>(p.resid);
+    T old[MT][16];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t m = 32 * mt + acc_row(i, lane);
+        old[mt][i] = rb[(ncol && m < p.M) ? m * p.ldr + n : 0];
+      }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t m = 32 * mt + acc_row(i, lane);
+        if (ncol && m < p.M)
+          rb[m * p.ldr + n] = Ty<DT>::from(Ty<DT>::f(old[mt][i]) + Ty<DT>::f(Ty<DT>::from(acc[mt][i])));
+      }
+  } else {
+    if (n < p.n_conv) {
+      T4* const sb = static_cast<T4*>(p.conv_state);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int64_t m = 32 * mt + acc_row(i, lane);
+          if (m >= p.M) continue;
+          const T xr = Ty<DT>::from(acc[mt][i]);
+          float a = bias;
+          a = __builtin_fmaf(Ty<DT>::f(cw[0]), Ty<DT>::f(win[mt][i][1]), a);
+          a = __builtin_fmaf(Ty<DT>::f(cw[1]), Ty<DT>::f(win[mt][i][2]), a);
+          a = __builtin_fmaf(Ty<DT>::f(cw[2]), Ty<DT>::f(win[mt][i][3]), a);
+          a = __builtin_fmaf(Ty<DT>::f(cw[3]), Ty<DT>::f(xr), a);
+          T4 nw;
+          nw[0] = win[mt][i][1];
+          nw[1] = win[mt][i][2];
+          nw[2] = win[mt][i][3];
+          nw[3] = xr;
+          sb[m * p.n_conv + n] = nw;
+          st<DT>(p.conv_out, m * p.ldc + n, silu_f(a));
+        }
+    } else if (ncol) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int64_t m = 32 * mt + acc_row(i, lane);
+          if (m < p.M) st<DT>(p.y, m * p.ldy + (n - p.n_conv), acc[mt][i]);
+        }
+    }
+  }
+}
+
 // Split calls, second pass: y = sum over splits (in order) of the fp32 partials,
 // then the epilogue.  One thread per 4 consecutive columns of a row; the KS loads
 // of a thread are all issued before the sum (KS is a template parameter).
@@ -485,6 +672,34 @@ void launch_main(const LinParams& p, int32_t epi, const Plan& pl, dim3 grid, hip
   else if (two) launch_ksw<DT, 2, 1>(p, epi, pl.ksw, grid, s);
   else if (pl.nt == 2) launch_ksw<DT, 1, 2>(p, epi, pl.ksw, grid, s);
   else launch_ksw<DT, 1, 1>(p, epi, pl.ksw, grid, s);
+}
+
+template <int DT, int NW, int MT>
+void launch_share_epi(const LinParams& p, int32_t epi, dim3 grid, hipStream_t s) {
+  const dim3 block(NW * 64);
+  switch (epi) {
+    case MM_LIN_STORE:
+      hipLaunchKernelGGL((share_kernel<DT, NW, MT, MM_LIN_STORE>), grid, block, 0, s, p);
+      break;
+    case MM_LIN_RESID:
+      hipLaunchKernelGGL((share_kernel<DT, NW, MT, MM_LIN_RESID>), grid, block, 0, s, p);
+      break;
+    default:
+      hipLaunchKernelGGL((share_kernel<DT, NW, MT, MM_LIN_CONV>), grid, block, 0, s, p);
+      break;
+  }
+}
+
+template <int DT, int MT>
+void launch_share_nw(const LinParams& p, int32_t epi, int nw, dim3 grid, hipStream_t s) {
+  if (nw == 4) launch_share_epi<DT, 4, MT>(p, epi, grid, s);
+  else launch_share_epi<DT, 8, MT>(p, epi, grid, s);
+}
+
+template <int DT>
+void launch_share(const LinParams& p, int32_t epi, const Plan& pl, dim3 grid, hipStream_t s) {
+  if (p.M > 32) launch_share_nw<DT, 2>(p, epi, pl.nw, grid, s);
+  else launch_share_nw<DT, 1>(p, epi, pl.nw, grid, s);
 }
 
 template <int DT, int EPI>
@@ -647,13 +862,17 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
   p.ldc = q.ldc;
   p.n_conv = q.n_conv;
   p.ks = pl.ks;
-  const dim3 grid(static_cast<unsigned>(ceil_div(q.N, kTileN * pl.nt)), static_cast<unsigned>(pl.ks));
+  const dim3 grid(static_cast<unsigned>(ceil_div(q.N, kTileN * (pl.nw > 0 ? pl.nw : pl.nt))),
+                  static_cast<unsigned>(pl.ks));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool norm = q.epilogue == MM_LIN_RESID_NORM;
   const bool fused_norm = norm && fused_norm_ok(p, q.dtype, q.resid, q.norm_w, q.norm_out);
   const int32_t epi = norm ? MM_LIN_RESID : q.epilogue;  // RESID_NORM = RESID + norm pass
   const int32_t main_epi = pl.ks > 1 ? kPartial : epi;
-  if (q.dtype == MM_F16) {
+  if (pl.nw > 0) {
+    if (q.dtype == MM_F16) launch_share<MM_F16>(p, epi, pl, grid, s);
+    else launch_share<MM_BF16>(p, epi, pl, grid, s);
+  } else if (q.dtype == MM_F16) {
     launch_main<MM_F16>(p, main_epi, pl, grid, s);
     if (fused_norm) launch_reduce_norm<MM_F16>(p, s);
     else if (pl.ks > 1) launch_reduce<MM_F16>(p, epi, s);

@@ -29,11 +29,16 @@ def _check(got, ref, dtype, what):
 # decode shapes of Mamba-2.8B (in/out/x projections, head) and 130M, ragged M/N,
 # split-K (narrow N) and single-chunk K
 # (37, 4096, 100) and (64, 5120, 192) split K over the grid with ragged / narrow N; the
-# 130M batch-1 shapes and the small ones keep K in the workgroup
+# 130M batch-1 shapes and the small ones keep K in the workgroup; (64, 2560, 10240) and
+# (20, 128, 8200) give each wave two column tiles.  > 512 column tiles run the shared-X
+# kernel: (37, 256, 20000) with 4 waves and a ragged last tile, (64, 2560, 50280) and
+# (1, 768, 50280) (130M head at batch 1: one 32-row MFMA tile, X staged by half the
+# waves) with 8.
 @pytest.mark.parametrize("M,K,N", [(64, 2560, 10240), (64, 5120, 2560), (64, 5120, 192),
                                    (1, 768, 3072), (1, 1536, 80), (37, 1536, 100), (33, 256, 50),
                                    (37, 4096, 100), (32, 64, 33), (64, 2560, 50280), (5, 64, 7),
-                                   (64, 64, 4096)])
+                                   (64, 64, 4096), (1, 768, 50280), (37, 256, 20000),
+                                   (20, 128, 8200)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_decode_linear(dev, M, K, N, dtype):
     from mamba_metal_amd.linear import decode_linear
@@ -91,12 +96,13 @@ def test_decode_linear_strided_rows(dev):
     assert torch.count_nonzero(outbuf[:, 300:]) == 0      # nothing written past N
 
 
+# (64, 5120, 2560): 2.8B out_proj (split K); (40, 128, 16600): shared-X kernel, ragged
+@pytest.mark.parametrize("M,K,N", [(64, 5120, 2560), (40, 128, 16600)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_decode_linear_resid(dev, dtype):
+def test_decode_linear_resid(dev, M, K, N, dtype):
     from mamba_metal_amd.linear import decode_linear_resid_
 
-    g = torch.Generator(device=dev).manual_seed(2)
-    M, K, N = 64, 5120, 2560
+    g = torch.Generator(device=dev).manual_seed(2 + N)
     y = torch.randn((M, K), generator=g, device=dev).to(dtype)
     w = (torch.randn((N, K), generator=g, device=dev) * 0.02).to(dtype)
     resid = torch.randn((M, N), generator=g, device=dev).to(dtype)
@@ -138,14 +144,16 @@ def test_decode_linear_resid_norm(dev, M, K, N, dtype):
     assert_close(out.float().cpu().numpy(), ref, TOL[dtype], TOL[dtype], f"norm M={M} N={N}")
 
 
+# di = 1536: 130M shape; di = 5120: 2.8B width (two column tiles per wave); di = 8300
+# (the conv / z boundary inside a 32-column tile): > 512 column tiles, shared-X kernel
+@pytest.mark.parametrize("K,di", [(768, 1536), (256, 5120), (128, 8300)])
 @pytest.mark.parametrize("M", [64, 3])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_decode_in_proj_conv(dev, M, dtype):
+def test_decode_in_proj_conv(dev, K, di, M, dtype):
     """in_proj + conv-window step == GEMM, then the oracle's decode conv step."""
     from mamba_metal_amd.linear import decode_in_proj_conv
 
-    g = torch.Generator(device=dev).manual_seed(3 + M)
-    K, di = 768, 1536
+    g = torch.Generator(device=dev).manual_seed(3 + M + di)
     x = torch.randn((M, K), generator=g, device=dev).to(dtype)
     w = (torch.randn((2 * di, K), generator=g, device=dev) * 0.05).to(dtype)
     cw = torch.randn((di, 1, 4), generator=g, device=dev).to(dtype)
