@@ -34,9 +34,6 @@
 namespace mm {
 namespace scan {
 
-#ifndef MM_SCAN_PF
-#define MM_SCAN_PF 1
-#endif
 #ifndef MM_SCAN_G16
 #define MM_SCAN_G16 8
 #endif
@@ -45,11 +42,15 @@ namespace scan {
 #endif
 
 constexpr int kCPW = 64;     // channels per workgroup (lanes per wave)
-// Tiles of u/delta/z/B/C loaded ahead of the scan (1 or 2).
-constexpr int kPF = MM_SCAN_PF;
-static_assert(kPF == 1 || kPF == 2, "prefetch depth");
 constexpr int kT = 32;       // timesteps per tile
 constexpr int kTP = kT + 4;  // padded LDS row length (floats)
+// The sequence is padded to whole groups of four tiles (the tile loop is unrolled by
+// four, without guards); padded steps are identity steps (delta' = 0, B = C = 0).
+constexpr int kTGroup = 4;
+
+inline int64_t padded_len(int64_t seqlen) {
+  return round_up(seqlen > 1 ? seqlen : 1, kTGroup * kT);
+}
 constexpr int kSpinLimit = 1 << 26;
 
 enum Layout { kTimeContig = 0, kChanContig = 1 };
@@ -80,7 +81,7 @@ inline WsLayout ws_layout(int64_t batch, int64_t dim, int64_t groups, int64_t sp
   w.flags = 256;
   w.carry = static_cast<size_t>(round_up(w.flags + 4 * ncb, 256));
   w.bc = static_cast<size_t>(round_up(w.carry + 4 * ncb * groups * spl * kCPW, 256));
-  w.total = w.bc + static_cast<size_t>(4 * batch * groups * round_up(seqlen, kT) * 2 * spl);
+  w.total = w.bc + static_cast<size_t>(4 * batch * groups * padded_len(seqlen) * 2 * spl);
   return w;
 }
 
@@ -231,26 +232,33 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
       Dv[j] = (p.D != nullptr && d < p.dim) ? p.D[d * p.Ds] : 0.0f;
     }
 
-    // Prefetch slots: named variables passed by reference to always-inlined lambdas, so
-    // they stay in registers (an array indexed by slot would be moved to LDS).
-    VE ru0, rd0, rz0, ru1, rd1, rz1;
-    float4 rbc0[BCPT], rbc1[BCPT];
+    // Input tiles are loaded in pairs, two tiles ahead: the loads of tiles 2k and 2k+1
+    // are issued together, in the prologue of tile 2k-2.  With 2-byte inputs along time
+    // a 32-step tile is half of each channel row's 128-byte line; requesting both
+    // halves back to back means no line has to survive in L2 between tiles (rows
+    // 2^k bytes apart share L2 sets, and the y stores push such lines out).
+    // Slots are named variables passed by reference to always-inlined lambdas, so they
+    // stay in registers (an array indexed by slot would be moved to LDS).
+    VE ru0, rd0, rz0, ru1, rd1, rz1, ru2, rd2, rz2, ru3, rd3, rz3;
+    float4 rbc0[BCPT], rbc1[BCPT], rbc2[BCPT], rbc3[BCPT];
+#define MM_SLOT(i) ru##i, rd##i, rz##i, rbc##i
     // All loads are unconditional from clamped, in-bounds addresses (elements outside
-    // the tensors read element (b, 0, 0); z, when absent, reads u): the prologue masks
-    // those elements and the epilogue never stores them.  Guarded loads would make
-    // the compiler wait for every outstanding load at the first use, which defeats
-    // the kPF-deep prefetch.
+    // the tensors read element (b, 0, 0); z, when absent, reads u; steps past the padded
+    // length read step 0 of B/C): the prologue masks those elements and the epilogue
+    // never stores them.  Guarded loads would make the compiler wait for every
+    // outstanding load at the first use, which defeats the prefetch.
     const T* const zsrc = static_cast<const T*>(has_z ? z_ : u_);
     const int64_t zs0 = has_z ? p.zs0 : p.us0, zs1 = has_z ? p.zs1 : p.us1,
                   zs2 = has_z ? p.zs2 : p.us2;
     auto load_raw = [&](VE& ru, VE& rd, VE& rz, float4 (&rbc)[BCPT], int64_t t0)
                         __attribute__((always_inline)) {
+      const int64_t tb = t0 < p.Lp ? t0 : 0;
 #pragma unroll
       for (int i = 0; i < BCPT; ++i) {
         const int v = (tid + i * NT) % BCV;
         const int gg = v / (kT * 2 * SPL / 4), rest = v % (kT * 2 * SPL / 4);
         rbc[i] = *reinterpret_cast<const float4*>(
-            bc_ + ((b * G + gg) * p.Lp + t0) * (2 * SPL) + rest * 4);
+            bc_ + ((b * G + gg) * p.Lp + tb) * (2 * SPL) + rest * 4);
       }
       if constexpr (VEC) {
         const bool in = (d0 + vc < p.dim) && (t0 + vt < p.seqlen);
@@ -270,8 +278,8 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
       }
     };
 
-    load_raw(ru0, rd0, rz0, rbc0, tile0 * kT);
-    if (kPF > 1 && tile0 + 1 < tile1) load_raw(ru1, rd1, rz1, rbc1, (tile0 + 1) * kT);
+    load_raw(MM_SLOT(0), tile0 * kT);
+    load_raw(MM_SLOT(1), (tile0 + 1) * kT);
 
     // ---- carried state from the previous segment of this chain ----
     if (seg > 0) {
@@ -293,8 +301,12 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
         h[k] = __hip_atomic_load(cp + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    auto process = [&](VE& ru, VE& rd, VE& rz, float4 (&rbc)[BCPT], int64_t tile)
-                       __attribute__((always_inline)) {
+    // process(slot, tile, slot a, slot b, issue): scan tile from the first slot; with
+    // issue, load tiles tile + 2 and tile + 3 into slots a and b (both free: consumed
+    // two tiles ago).
+    auto process = [&](VE& ru, VE& rd, VE& rz, float4 (&rbc)[BCPT], int64_t tile, VE& uA, VE& dA,
+                       VE& zA, float4 (&bcA)[BCPT], VE& uB, VE& dB, VE& zB, float4 (&bcB)[BCPT],
+                       bool issue) __attribute__((always_inline)) {
       const int64_t t0 = tile * kT;
       const bool full = (t0 + kT <= p.seqlen) && (d0 + kCPW <= p.dim);
 
@@ -336,7 +348,10 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
         const int v = tid + i * NT;
         if (v < BCV) reinterpret_cast<float4*>(&s_bc[0][0][0])[v] = rbc[i];
       }
-      if (tile + kPF < tile1) load_raw(ru, rd, rz, rbc, t0 + kPF * kT);  // in flight during the scans
+      if (issue) {  // in flight during the next two tiles' scans
+        load_raw(uA, dA, zA, bcA, t0 + 2 * kT);
+        load_raw(uB, dB, zB, bcB, t0 + 3 * kT);
+      }
       __syncthreads();
 
       // ---- scan: lane = channel, wave = state group; LDS reads one group ahead ----
@@ -443,10 +458,15 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
         }
       }
     };
-    for (int64_t tile = tile0; tile < tile1; tile += kPF) {
-      process(ru0, rd0, rz0, rbc0, tile);
-      if (kPF > 1 && tile + 1 < tile1) process(ru1, rd1, rz1, rbc1, tile + 1);
+    // tile1 - tile0 is a multiple of kTGroup (padded length, whole-group segments)
+    static_assert(kTGroup == 4, "the loop below is unrolled by four");
+    for (int64_t tile = tile0; tile < tile1; tile += kTGroup) {
+      process(MM_SLOT(0), tile, MM_SLOT(2), MM_SLOT(3), true);
+      process(MM_SLOT(1), tile + 1, MM_SLOT(2), MM_SLOT(3), false);
+      process(MM_SLOT(2), tile + 2, MM_SLOT(0), MM_SLOT(1), true);
+      process(MM_SLOT(3), tile + 3, MM_SLOT(0), MM_SLOT(1), false);
     }
+#undef MM_SLOT
 
     // ---- hand the state on, or write the final state ----
     if (seg + 1 < p.nseg) {
@@ -655,14 +675,16 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
   p.dim = a->dim;
   p.dstate = a->dstate;
   p.seqlen = a->seqlen;
-  p.Lp = round_up(std::max<int64_t>(a->seqlen, 1), kT);
+  p.Lp = padded_len(a->seqlen);
   p.nblk_d = ceil_div(a->dim, kCPW);
   p.ncb = a->batch * p.nblk_d;
   const int64_t ntiles = p.Lp / kT;
   // Segments: enough units that ~16 rounds keep every CU busy; at least 16 tiles each.
   const int64_t target_units = static_cast<int64_t>(num_cus()) * 16;
   int64_t nseg = std::max<int64_t>(1, std::min<int64_t>(ceil_div(target_units, p.ncb), ntiles / 16));
-  p.seg_tiles = ceil_div(ntiles, nseg);
+  // Whole groups of four tiles per segment: load pairs stay on whole lines and the
+  // unrolled tile loop needs no guards.
+  p.seg_tiles = round_up(ceil_div(ntiles, nseg), kTGroup);
   p.nseg = ceil_div(ntiles, p.seg_tiles);
   p.nunits = p.ncb * p.nseg;
   p.us0 = a->u_stride[0]; p.us1 = a->u_stride[1]; p.us2 = a->u_stride[2];
