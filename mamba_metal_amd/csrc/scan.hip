@@ -250,22 +250,37 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
     const T* const zsrc = static_cast<const T*>(has_z ? z_ : u_);
     const int64_t zs0 = has_z ? p.zs0 : p.us0, zs1 = has_z ? p.zs1 : p.us1,
                   zs2 = has_z ? p.zs2 : p.us2;
+    // Per-unit bases, so that a tile only adds its step offset: the vector path has unit
+    // stride along its contiguous axis (time for time-contiguous inputs); rows past dim
+    // read channel 0.  B/C: this thread's float4 slots of the packed tile.
+    const float* bcb[BCPT];
+#pragma unroll
+    for (int i = 0; i < BCPT; ++i) {
+      const int v = (tid + i * NT) % BCV;
+      const int gg = v / (kT * 2 * SPL / 4), rest = v % (kT * 2 * SPL / 4);
+      bcb[i] = bc_ + (b * G + gg) * p.Lp * (2 * SPL) + rest * 4;
+    }
+    const int64_t dcl = (d0 + vc < p.dim) ? d0 + vc : 0;
+    const T* const ub = static_cast<const T*>(u_) + b * p.us0 + dcl * p.us1;
+    const T* const db = static_cast<const T*>(delta_) + b * p.ds0 + dcl * p.ds1;
+    const T* const zb = zsrc + b * zs0 + dcl * zs1;
     auto load_raw = [&](VE& ru, VE& rd, VE& rz, float4 (&rbc)[BCPT], int64_t t0)
                         __attribute__((always_inline)) {
       const int64_t tb = t0 < p.Lp ? t0 : 0;
 #pragma unroll
-      for (int i = 0; i < BCPT; ++i) {
-        const int v = (tid + i * NT) % BCV;
-        const int gg = v / (kT * 2 * SPL / 4), rest = v % (kT * 2 * SPL / 4);
-        rbc[i] = *reinterpret_cast<const float4*>(
-            bc_ + ((b * G + gg) * p.Lp + tb) * (2 * SPL) + rest * 4);
-      }
+      for (int i = 0; i < BCPT; ++i)
+        rbc[i] = *reinterpret_cast<const float4*>(bcb[i] + tb * (2 * SPL));
       if constexpr (VEC) {
-        const bool in = (d0 + vc < p.dim) && (t0 + vt < p.seqlen);
-        const int64_t dc = in ? d0 + vc : 0, tc = in ? t0 + vt : 0;
-        ru = *reinterpret_cast<const VE*>(static_cast<const T*>(u_) + b * p.us0 + dc * p.us1 + tc * p.us2);
-        rd = *reinterpret_cast<const VE*>(static_cast<const T*>(delta_) + b * p.ds0 + dc * p.ds1 + tc * p.ds2);
-        rz = *reinterpret_cast<const VE*>(zsrc + b * zs0 + dc * zs1 + tc * zs2);
+        const int64_t tc = (t0 + vt < p.seqlen) ? t0 + vt : 0;
+        if constexpr (LAYOUT == kTimeContig) {  // unit stride along time
+          ru = *reinterpret_cast<const VE*>(ub + tc);
+          rd = *reinterpret_cast<const VE*>(db + tc);
+          rz = *reinterpret_cast<const VE*>(zb + tc);
+        } else {
+          ru = *reinterpret_cast<const VE*>(ub + tc * p.us2);
+          rd = *reinterpret_cast<const VE*>(db + tc * p.ds2);
+          rz = *reinterpret_cast<const VE*>(zb + tc * zs2);
+        }
       } else {
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
@@ -446,9 +461,9 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
 #pragma unroll
       for (int j = 0; j < EPT; ++j) ry[j] = Ty<DT>::from(yv[j] * gate[j]);
       if constexpr (VEC) {
-        if ((d0 + vc < p.dim) && (t0 + vt < p.seqlen))
-          *reinterpret_cast<VE*>(static_cast<T*>(y_) + b * p.ys0 + (d0 + vc) * p.ys1 +
-                                 (t0 + vt) * p.ys2) = ry;
+        T* const yp = static_cast<T*>(y_) + b * p.ys0 + (d0 + vc) * p.ys1 +
+                      (LAYOUT == kTimeContig ? t0 + vt : (t0 + vt) * p.ys2);
+        if ((d0 + vc < p.dim) && (t0 + vt < p.seqlen)) *reinterpret_cast<VE*>(yp) = ry;
       } else {
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
