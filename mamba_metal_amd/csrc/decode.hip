@@ -194,6 +194,7 @@ struct FusedParams {
   int64_t batch, dim, rank;
   int64_t xsb, dtsb, wsc, Bsb, Csb, zsb, ysb;
   int32_t wvec;  // W rows 16-byte aligned and rank % 8 == 0: 8-element vector loads
+  int32_t mvec;  // also dt_in rows 16-byte aligned (2-byte types): matrix-core dt projection
 };
 
 // 8 consecutive elements at p (16-byte aligned for 2-byte types, 32 for fp32).
@@ -345,6 +346,161 @@ __global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_dtproj_kernel(const
   }
 }
 
+// f16/bf16 variant with the dt projection on the matrix cores.  Workgroup = two waves =
+// 32 channels x kMBB batch rows.  Wave w:
+//   1. dt_pre[16 rows][16 channels] = dt_in[b0.., :] . W[c0 + 16w.., :]^T with KS
+//      v_mfma_f32_16x16x32 steps (lane l: A = dt_in row l%16, B = W row l%16, k slice
+//      8(l/16) .. +8 of each 32-wide step; C: rows 4(l/16) + i, column l%16);
+//   2. the tile goes through a wave-private LDS block into the update layout:
+//      lane l = channel l/4, states 4(l%4) .. +3, all kMBB rows;
+//   3. the update of `ssm_step_dtproj_kernel` per row.
+// All global loads are issued before the MFMAs (operands first, then the kMBB state
+// rows, x and z), from clamped in-bounds addresses; masked values never reach a store.
+// Batch rows per workgroup: 8 (measured faster than 16 on MI355X -- more, shorter
+// workgroups overlap their state reads and writes better); the 16-row dt tile's
+// upper half is computed and ignored.
+constexpr int kMBB = 8;
+static_assert(kMBB == 8 || kMBB == 16, "the dt tile has 16 rows");
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (DT == MM_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                   c, 0, 0, 0);
+}
+
+template <int DT, int KS>
+__global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_mfma_kernel(const FusedParams p) {
+  using T = typename Ty<DT>::T;
+  __shared__ float s_B[kMBB][kFusedNS];
+  __shared__ float s_C[kMBB][kFusedNS];
+  __shared__ float s_dt[kFusedWaves][16][17];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t cw0 = static_cast<int64_t>(blockIdx.x) * kFusedCh + wave * 16;  // wave's channels
+  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * kMBB;
+  const int R = static_cast<int>(p.rank);
+
+  // ---- MFMA operands: dt_in row b0 + l%16, W row cw0 + l%16, k = 32 s + 8(l/16) ----
+  const int64_t ar = b0 + (lane & 15) < p.batch ? b0 + (lane & 15) : 0;
+  const int64_t wr = cw0 + (lane & 15) < p.dim ? cw0 + (lane & 15) : 0;
+  const int kl = 8 * (lane >> 4);
+  u32x4 av[KS], bv[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int k = 32 * s + kl < R ? 32 * s + kl : 0;
+    av[s] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.dt_in) + ar * p.dtsb + k);
+    bv[s] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.w) + wr * p.wsc + k);
+  }
+  // ---- B / C rows of this workgroup (staged in LDS), then the per-lane update inputs ----
+  constexpr int NBCU = kMBB * kFusedNS / (kFusedWaves * 64);
+  T bcr[NBCU];
+#pragma unroll
+  for (int u = 0; u < NBCU; ++u) {
+    const int e = tid + u * kFusedWaves * 64;  // rows x 16 states
+    const int bb = e >> 4, n = e & 15;
+    const int64_t row = b0 + bb < p.batch ? b0 + bb : 0;
+    bcr[u] = static_cast<const T*>(p.B)[row * p.Bsb + n];
+  }
+  T ccr[NBCU];
+#pragma unroll
+  for (int u = 0; u < NBCU; ++u) {
+    const int e = tid + u * kFusedWaves * 64;
+    const int bb = e >> 4, n = e & 15;
+    const int64_t row = b0 + bb < p.batch ? b0 + bb : 0;
+    ccr[u] = static_cast<const T*>(p.C)[row * p.Csb + n];
+  }
+  const int q = lane & 3;
+  const int cl = lane >> 2;
+  const int64_t c = cw0 + cl;
+  const bool cok = c < p.dim;
+  const int64_t cc = cok ? c : 0;
+  const float4 Av = *reinterpret_cast<const float4*>(p.A + cc * kFusedNS + q * 4);
+  const T biasr = static_cast<const T*>(p.bias ? p.bias : p.x)[p.bias ? cc : 0];
+  const float Dr = p.D ? p.D[cc] : 0.0f;
+  const T* const zp = static_cast<const T*>(p.z ? p.z : p.x);
+  float4 hv[kMBB];
+  T xr[kMBB], zr[kMBB];
+#pragma unroll
+  for (int bb = 0; bb < kMBB; ++bb) {
+    const int64_t b = b0 + bb < p.batch ? b0 + bb : 0;
+    hv[bb] = *reinterpret_cast<const float4*>(p.h + (b * p.dim + cc) * kFusedNS + q * 4);
+    xr[bb] = static_cast<const T*>(p.x)[b * p.xsb + cc];
+    zr[bb] = zp[p.z ? b * p.zsb + cc : b * p.xsb + cc];
+  }
+
+  // ---- dt_pre on the matrix cores (k past rank contributes zero) ----
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    u32x4 a = av[s], w = bv[s];
+    if (32 * s + kl >= R) a = u32x4{0u, 0u, 0u, 0u}, w = a;
+    acc = mfma16<DT>(a, w, acc);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s_dt[wave][4 * (lane >> 4) + i][lane & 15] = acc[i];
+#pragma unroll
+  for (int u = 0; u < NBCU; ++u) {
+    const int e = tid + u * kFusedWaves * 64;
+    (&s_B[0][0])[e] = Ty<DT>::f(bcr[u]);
+    (&s_C[0][0])[e] = Ty<DT>::f(ccr[u]);
+  }
+  __syncthreads();
+
+  // ---- update: lane = (channel cl, states 4q .. 4q+3), rows b0 .. b0 + kMBB - 1 ----
+  const float Al[4] = {Av.x * kLog2e, Av.y * kLog2e, Av.z * kLog2e, Av.w * kLog2e};
+  const float bias = p.bias ? Ty<DT>::f(biasr) : 0.0f;
+  float* const hw = p.h + (b0 * p.dim + cc) * kFusedNS + q * 4;
+#pragma unroll
+  for (int bb = 0; bb < kMBB; ++bb) {
+    if (b0 + bb >= p.batch) break;
+    const float xv = Ty<DT>::f(xr[bb]);
+    const float dtv = softplus_full(s_dt[wave][bb][cl] + bias);
+    const float du = dtv * xv;
+    float hs[4] = {hv[bb].x, hv[bb].y, hv[bb].z, hv[bb].w};
+    float yacc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float a = exp2_hw(dtv * Al[k]);
+      hs[k] = __builtin_fmaf(a, hs[k], du * s_B[bb][q * 4 + k]);
+      yacc = __builtin_fmaf(hs[k], s_C[bb][q * 4 + k], yacc);
+    }
+    if (cok) *reinterpret_cast<float4*>(hw + bb * p.dim * kFusedNS) = make_float4(hs[0], hs[1], hs[2], hs[3]);
+    yacc += __shfl_xor(yacc, 1, 64);
+    yacc += __shfl_xor(yacc, 2, 64);
+    if (q == 0 && cok) {
+      yacc = __builtin_fmaf(Dr, xv, yacc);
+      if (p.z) yacc *= silu_f(Ty<DT>::f(zr[bb]));
+      st<DT>(p.y, (b0 + bb) * p.ysb + c, yacc);
+    }
+  }
+}
+
+template <int DT>
+void launch_mfma(const FusedParams& p, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(ceil_div(p.dim, kFusedCh)),
+                  static_cast<unsigned>(ceil_div(p.batch, kMBB)));
+  const dim3 block(kFusedWaves * 64);
+  switch (ceil_div(p.rank, 32)) {
+    case 1: hipLaunchKernelGGL((ssm_step_mfma_kernel<DT, 1>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((ssm_step_mfma_kernel<DT, 2>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((ssm_step_mfma_kernel<DT, 3>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((ssm_step_mfma_kernel<DT, 4>), grid, block, 0, s, p); break;
+    case 5: hipLaunchKernelGGL((ssm_step_mfma_kernel<DT, 5>), grid, block, 0, s, p); break;
+    case 6: hipLaunchKernelGGL((ssm_step_mfma_kernel<DT, 6>), grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL((ssm_step_mfma_kernel<DT, 8>), grid, block, 0, s, p); break;
+  }
+}
+
 template <int DT, bool WV>
 void launch_fused_w(const FusedParams& p, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(ceil_div(p.dim, kFusedCh)),
@@ -363,7 +519,8 @@ void launch_fused_w(const FusedParams& p, hipStream_t s) {
 
 template <int DT>
 void launch_fused(const FusedParams& p, hipStream_t s) {
-  if (p.wvec) launch_fused_w<DT, true>(p, s);
+  if (DT != MM_F32 && p.mvec) launch_mfma<DT == MM_F32 ? MM_F16 : DT>(p, s);
+  else if (p.wvec) launch_fused_w<DT, true>(p, s);
   else launch_fused_w<DT, false>(p, s);
 }
 
@@ -423,6 +580,7 @@ int mm_decode_ssm_step_dtproj(float* ssm_state, const void* x, const void* dt_in
     const int64_t vb = x_dtype == MM_F32 ? 32 : 16;  // bytes of 8 elements
     const int64_t es = dtype_size(x_dtype);
     p.wvec = (rank % 8 == 0) && aligned(dt_weight, vb) && ((w_stride_c * es) % vb == 0) ? 1 : 0;
+    p.mvec = (p.wvec && x_dtype != MM_F32 && aligned(dt_in, 16) && (dt_stride_b * es) % 16 == 0) ? 1 : 0;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (x_dtype) {
