@@ -59,11 +59,12 @@ def test_decode_linear(dev, M, K, N, dtype):
 
 def test_decode_linear_split_sequence(dev):
     """Split-K calls of different shapes in a row share one partials workspace; each
-    must be right whatever the previous call left there."""
+    must be right whatever the previous call left there (narrow and wide calls mixed)."""
     from mamba_metal_amd.linear import decode_linear
 
     g = torch.Generator(device=dev).manual_seed(11)
-    for (M, K, N) in [(64, 5120, 192), (37, 4096, 100), (64, 5120, 192), (33, 5120, 2000)]:
+    for (M, K, N) in [(64, 5120, 192), (37, 4096, 100), (64, 5120, 192), (64, 5120, 2560),
+                      (33, 5120, 2000), (64, 5120, 2560)]:
         x = torch.randn((M, K), generator=g, device=dev).half()
         w = (torch.randn((N, K), generator=g, device=dev) * 0.05).half()
         _check(decode_linear(x, w), _ref(x, w), torch.float16, f"sequence M={M} K={K} N={N}")
