@@ -204,6 +204,33 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
   const int wr_off = (lane >> 3) * kRowBytes + (lane & 7) * 16;
   const int rd_off = (lane & 31) * kRowBytes + (lane >> 5) * 16;
 
+  // Epilogue ownership (reduced tile element e = row * TN + col, e = tid + u * KSW * 64):
+  // the column is the same for all of a thread's elements (KSW * 64 is a multiple of TN),
+  // the rows step by KSW * 64 / TN.  The conv epilogue's inputs (window, weights, bias)
+  // do not depend on the product: they are loaded before the K loop so their latency
+  // hides under it (clamped: elements outside the conv half read column 0, row 0).
+  constexpr int EPT = EPI == kPartial ? 1 : MT * 32 * TN / (KSW * 64);
+  static_assert(EPI == kPartial || (KSW * 64) % TN == 0, "epilogue column per thread");
+  const int e_col = threadIdx.x % TN;
+  const int e_row0 = threadIdx.x / TN;
+  constexpr int kRowStep = KSW * 64 / TN;
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  T4 win[EPI == MM_LIN_CONV ? EPT : 1];
+  T4 cw{};
+  float cbias = 0.0f;
+  if constexpr (EPI == MM_LIN_CONV) {
+    const int64_t n = n0 + e_col;
+    const int64_t nc = n < p.n_conv ? n : 0;
+    const T4* const sb = static_cast<const T4*>(p.conv_state);
+#pragma unroll
+    for (int u = 0; u < EPT; ++u) {
+      const int64_t m = e_row0 + u * kRowStep;
+      win[u] = sb[(m < p.M ? m : 0) * p.n_conv + nc];
+    }
+    cw = static_cast<const T4*>(p.conv_w)[nc];
+    if (p.conv_b) cbias = Ty<DT>::f(static_cast<const T*>(p.conv_b)[nc]);
+  }
+
   f32x16 acc[MT][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -278,15 +305,13 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
         for (int i = 0; i < 16; ++i) part[((mt * NT + j) * 16 + i) * 64 + lane] = acc[mt][j][i];
     __syncthreads();
     // Tile element e = row * TN + col, summed over the waves in order.  Each thread
-    // takes EPT elements; the epilogue's own loads (residual, conv window, conv
-    // weights) for all of them are issued before any of them is used.
-    constexpr int EPT = MT * 32 * TN / (KSW * 64);
+    // takes EPT elements; the residual loads for all of them are issued before any
+    // of them is used.
     float vals[EPT];
     int64_t ms[EPT], ns[EPT];
 #pragma unroll
     for (int u = 0; u < EPT; ++u) {
-      const int e = threadIdx.x + u * KSW * 64;
-      const int row = e / TN, col = e % TN;
+      const int row = e_row0 + u * kRowStep, col = e_col;
       const int rr = row & 31;
       const int reg = (((row >> 5) * NT + (col >> 5)) * 16) + 4 * (rr >> 3) + (rr & 3);
       const int ln = (col & 31) + 32 * ((rr >> 2) & 1);
@@ -315,31 +340,18 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
         if (ms[u] < p.M && ns[u] < p.N)
           rb[ms[u] * p.ldr + ns[u]] = Ty<DT>::from(Ty<DT>::f(old[u]) + Ty<DT>::f(Ty<DT>::from(vals[u])));
     } else {
-      typedef T T4 __attribute__((ext_vector_type(4)));
       T4* const sb = static_cast<T4*>(p.conv_state);
-      const T4* const wb = static_cast<const T4*>(p.conv_w);
-      const T* const bb = static_cast<const T*>(p.conv_b ? p.conv_b : p.conv_w);
-      T4 win[EPT], cw[EPT];
-      T bias[EPT];
-#pragma unroll
-      for (int u = 0; u < EPT; ++u) {
-        const bool ok = ms[u] < p.M && ns[u] < p.n_conv;
-        const int64_t mc = ok ? ms[u] : 0, nc = ok ? ns[u] : 0;
-        win[u] = sb[mc * p.n_conv + nc];
-        cw[u] = wb[nc];
-        bias[u] = bb[p.conv_b ? nc : 0];
-      }
 #pragma unroll
       for (int u = 0; u < EPT; ++u) {
         const int64_t m = ms[u], n = ns[u];
         if (m >= p.M || n >= p.N) continue;
         if (n < p.n_conv) {
           const T xr = Ty<DT>::from(vals[u]);
-          float a = p.conv_b ? Ty<DT>::f(bias[u]) : 0.0f;
-          a = __builtin_fmaf(Ty<DT>::f(cw[u][0]), Ty<DT>::f(win[u][1]), a);
-          a = __builtin_fmaf(Ty<DT>::f(cw[u][1]), Ty<DT>::f(win[u][2]), a);
-          a = __builtin_fmaf(Ty<DT>::f(cw[u][2]), Ty<DT>::f(win[u][3]), a);
-          a = __builtin_fmaf(Ty<DT>::f(cw[u][3]), Ty<DT>::f(xr), a);
+          float a = cbias;
+          a = __builtin_fmaf(Ty<DT>::f(cw[0]), Ty<DT>::f(win[u][1]), a);
+          a = __builtin_fmaf(Ty<DT>::f(cw[1]), Ty<DT>::f(win[u][2]), a);
+          a = __builtin_fmaf(Ty<DT>::f(cw[2]), Ty<DT>::f(win[u][3]), a);
+          a = __builtin_fmaf(Ty<DT>::f(cw[3]), Ty<DT>::f(xr), a);
           T4 nw;
           nw[0] = win[u][1];
           nw[1] = win[u][2];

@@ -42,7 +42,14 @@ namespace scan {
 #endif
 
 constexpr int kCPW = 64;     // channels per workgroup (lanes per wave)
-constexpr int kT = 32;       // timesteps per tile
+#ifndef MM_SCAN_KT
+#define MM_SCAN_KT 32
+#endif
+#ifndef MM_SCAN_MIN_WG
+#define MM_SCAN_MIN_WG 1
+#endif
+
+constexpr int kT = MM_SCAN_KT;  // timesteps per tile
 constexpr int kTP = kT + 4;  // padded LDS row length (floats)
 // The sequence is padded to whole groups of four tiles (the tile loop is unrolled by
 // four, without guards); padded steps are identity steps (delta' = 0, B = C = 0).
@@ -128,6 +135,18 @@ __global__ __launch_bounds__(256) void pack_bc_kernel(const void* __restrict__ B
   }
 }
 
+// float vectors of the prologue's LDS stores and the epilogue's LDS reads
+template <int W>
+struct FVec;
+template <>
+struct FVec<4> {
+  typedef float type __attribute__((ext_vector_type(4)));
+};
+template <>
+struct FVec<2> {
+  typedef float type __attribute__((ext_vector_type(2)));
+};
+
 template <int DT, int N>
 struct Vec;
 template <int DT>
@@ -158,7 +177,7 @@ __device__ __forceinline__ float softplus_log2(float x) {
 
 // ---------------------------------------------------------------------------
 template <int DT, int LAYOUT, int SPL, int G, bool VEC>
-__global__ __launch_bounds__(kCPW * G) void scan_kernel(
+__global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
     const Params p, const void* __restrict__ u_, const void* __restrict__ delta_,
     const void* __restrict__ z_, void* __restrict__ y_, const float* __restrict__ bc_,
     float* __restrict__ state_out_, int* __restrict__ ctl_, float* __restrict__ carry_) {
@@ -167,6 +186,8 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
   constexpr int EPT = kCPW * kT / NT;  // elements per thread per tile
   static_assert(EPT == 8 || EPT == 4 || EPT == 2, "tile split");
   using VE = typename Vec<DT, EPT>::type;
+  constexpr int VW = EPT >= 4 ? 4 : 2;  // floats per LDS vector access of the prologue/epilogue
+  using FV = typename FVec<VW>::type;
   constexpr int TPC = kT / EPT;        // threads per channel (time-contiguous mapping)
   constexpr int BCF = G * kT * 2 * SPL;  // floats of B/C per tile
   constexpr int BCV = BCF / 4;
@@ -345,18 +366,17 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
           duv[j] = in ? duv[j] : 0.0f;
         }
       }
-      if (LAYOUT == kTimeContig) {
 #pragma unroll
-        for (int j = 0; j < EPT; j += 4) {
-          *reinterpret_cast<float4*>(&s_dt[at(vc, vt + j)]) = make_float4(dtv[j], dtv[j + 1], dtv[j + 2], dtv[j + 3]);
-          *reinterpret_cast<float4*>(&s_du[at(vc, vt + j)]) = make_float4(duv[j], duv[j + 1], duv[j + 2], duv[j + 3]);
-        }
-      } else {
+      for (int j = 0; j < EPT; j += VW) {
+        FV dv, uv;
 #pragma unroll
-        for (int j = 0; j < EPT; j += 4) {
-          *reinterpret_cast<float4*>(&s_dt[at(vc + j, vt)]) = make_float4(dtv[j], dtv[j + 1], dtv[j + 2], dtv[j + 3]);
-          *reinterpret_cast<float4*>(&s_du[at(vc + j, vt)]) = make_float4(duv[j], duv[j + 1], duv[j + 2], duv[j + 3]);
+        for (int e = 0; e < VW; ++e) {
+          dv[e] = dtv[j + e];
+          uv[e] = duv[j + e];
         }
+        const int o = (LAYOUT == kTimeContig) ? at(vc, vt + j) : at(vc + j, vt);
+        *reinterpret_cast<FV*>(&s_dt[o]) = dv;
+        *reinterpret_cast<FV*>(&s_du[o]) = uv;
       }
 #pragma unroll
       for (int i = 0; i < BCPT; ++i) {
@@ -427,35 +447,21 @@ __global__ __launch_bounds__(kCPW * G) void scan_kernel(
       float yv[EPT];
 #pragma unroll
       for (int j = 0; j < EPT; ++j) yv[j] = yskip[j];
-      if (LAYOUT == kTimeContig) {
+      {
         // all G partial reads in flight before the (in-order) sum
-        float4 part[G][EPT / 4];
+        FV part[G][EPT / VW];
 #pragma unroll
         for (int gg = 0; gg < G; ++gg)
 #pragma unroll
-          for (int j = 0; j < EPT; j += 4)
-            part[gg][j / 4] = *reinterpret_cast<const float4*>(&s_y[gg][at(vc, vt + j)]);
+          for (int j = 0; j < EPT; j += VW)
+            part[gg][j / VW] = *reinterpret_cast<const FV*>(
+                &s_y[gg][(LAYOUT == kTimeContig) ? at(vc, vt + j) : at(vc + j, vt)]);
 #pragma unroll
         for (int gg = 0; gg < G; ++gg)
 #pragma unroll
-          for (int j = 0; j < EPT; j += 4) {
-            const float4 a = part[gg][j / 4];
-            yv[j] += a.x; yv[j + 1] += a.y; yv[j + 2] += a.z; yv[j + 3] += a.w;
-          }
-      } else {
-        float4 part[G][EPT / 4];
+          for (int j = 0; j < EPT; j += VW)
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg)
-#pragma unroll
-          for (int j = 0; j < EPT; j += 4)
-            part[gg][j / 4] = *reinterpret_cast<const float4*>(&s_y[gg][at(vc + j, vt)]);
-#pragma unroll
-        for (int gg = 0; gg < G; ++gg)
-#pragma unroll
-          for (int j = 0; j < EPT; j += 4) {
-            const float4 a = part[gg][j / 4];
-            yv[j] += a.x; yv[j + 1] += a.y; yv[j + 2] += a.z; yv[j + 3] += a.w;
-          }
+            for (int e = 0; e < VW; ++e) yv[j + e] += part[gg][j / VW][e];
       }
       VE ry;
 #pragma unroll
