@@ -541,6 +541,33 @@ int num_cus() {
   return cached[dev];
 }
 
+// Segments per chain.  A chain's segments run one after another (each waits for the
+// carried state of the previous one), so at most min(grid, chains) units run at once and
+// the makespan is about ceil(units / that) rounds of (seg_tiles + ~1 tile of per-unit
+// overhead: ticket, carry hand-off, pipeline fill).  Segments are whole groups of four
+// tiles (load pairs stay on whole lines; the unrolled tile loop needs no guards) and at
+// least 16 tiles where the sequence allows.  Among counts whose estimate is within 2% of
+// the best, the largest wins: finer units even out workgroups that run slower.
+inline void pick_segments(Params& p, int64_t grid) {
+  const int64_t ntiles = p.Lp / kT;
+  const int64_t par = std::max<int64_t>(1, std::min<int64_t>(grid, p.ncb));
+  const int64_t max_seg = std::max<int64_t>(1, std::min<int64_t>(64, ntiles / 16));
+  int64_t cost[65] = {0};
+  int64_t best = INT64_MAX;
+  for (int64_t n = 1; n <= max_seg; ++n) {
+    const int64_t st = round_up(ceil_div(ntiles, n), kTGroup);
+    const int64_t ns = ceil_div(ntiles, st);
+    cost[n] = (p.ncb * ns > (1LL << 30)) ? INT64_MAX : ceil_div(p.ncb * ns, par) * (st + 1);
+    best = std::min(best, cost[n]);
+  }
+  int64_t pick = 1;
+  for (int64_t n = 1; n <= max_seg; ++n)
+    if (cost[n] != INT64_MAX && cost[n] * 50 <= best * 51) pick = n;
+  p.seg_tiles = round_up(ceil_div(ntiles, pick), kTGroup);
+  p.nseg = ceil_div(ntiles, p.seg_tiles);
+  p.nunits = p.ncb * p.nseg;
+}
+
 template <int DT, int LAYOUT, int SPL, int G, bool VEC>
 void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w) {
   auto kern = scan_kernel<DT, LAYOUT, SPL, G, VEC>;
@@ -550,7 +577,9 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
   const float* bc = reinterpret_cast<const float*>(ws + w.bc);
   static int per_cu = 0;
   if (per_cu == 0) per_cu = resident_per_cu(kern, kCPW * G);
-  const int64_t grid = std::min<int64_t>(p.nunits, static_cast<int64_t>(num_cus()) * per_cu);
+  const int64_t resident = static_cast<int64_t>(num_cus()) * per_cu;
+  pick_segments(p, resident);
+  const int64_t grid = std::min<int64_t>(p.nunits, resident);
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(kCPW * G), 0, s, p, a->u,
                      a->delta, a->z, a->y, bc, a->state_out, ctl, carry);
 }
@@ -699,15 +728,7 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
   p.Lp = padded_len(a->seqlen);
   p.nblk_d = ceil_div(a->dim, kCPW);
   p.ncb = a->batch * p.nblk_d;
-  const int64_t ntiles = p.Lp / kT;
-  // Segments: enough units that ~16 rounds keep every CU busy; at least 16 tiles each.
-  const int64_t target_units = static_cast<int64_t>(num_cus()) * 16;
-  int64_t nseg = std::max<int64_t>(1, std::min<int64_t>(ceil_div(target_units, p.ncb), ntiles / 16));
-  // Whole groups of four tiles per segment: load pairs stay on whole lines and the
-  // unrolled tile loop needs no guards.
-  p.seg_tiles = round_up(ceil_div(ntiles, nseg), kTGroup);
-  p.nseg = ceil_div(ntiles, p.seg_tiles);
-  p.nunits = p.ncb * p.nseg;
+  // seg_tiles / nseg / nunits are set at launch, from the persistent grid size.
   p.us0 = a->u_stride[0]; p.us1 = a->u_stride[1]; p.us2 = a->u_stride[2];
   p.ds0 = a->delta_stride[0]; p.ds1 = a->delta_stride[1]; p.ds2 = a->delta_stride[2];
   if (a->z) {
