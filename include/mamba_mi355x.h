@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 1
+#define MM_ABI_VERSION 2
 /* Largest d_state accepted: mamba_metal/selective_scan.py:9 (MAX_DSTATE = 64). */
 #define MM_MAX_DSTATE 64
 
@@ -247,6 +247,14 @@ typedef struct mm_linear_params {
   float eps;              /* RESID_NORM */
   int32_t dtype;          /* MM_F16 or MM_BF16 */
   int32_t epilogue;       /* mm_linear_epilogue */
+  /* Optional input RMSNorm (NULL: off).  When set, x holds the raw residual rows
+   * and the product uses round(x * rsqrt(mean(x^2) + x_eps) * x_norm_w) -- the
+   * MambaResidualBlock.step norm of mamba_model.py:57 evaluated in the operand load,
+   * bit-identical to mm_add_rmsnorm's output.  (K,) in dtype, 16-byte aligned;
+   * M <= 8, K <= 4096 and N <= 16384. */
+  const void* x_norm_w;
+  float x_eps;
+  int32_t reserved;       /* must be 0 */
 } mm_linear_params;
 
 /* Bytes of the packed copy of an (N, K) weight: ceil(N/32)*32 * K elements. */

@@ -19,7 +19,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library; see module d
 
 LIB_NAME = "libmamba_mi355x.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 1
+ABI_VERSION = 2
 MAX_DSTATE = 64
 
 # mm_dtype
@@ -69,6 +69,7 @@ class LinearParams(ctypes.Structure):
         ("M", _i64), ("N", _i64), ("K", _i64),
         ("ldx", _i64), ("ldy", _i64), ("ldr", _i64), ("ldc", _i64), ("ldn", _i64),
         ("n_conv", _i64), ("eps", ctypes.c_float), ("dtype", _i32), ("epilogue", _i32),
+        ("x_norm_w", _vp), ("x_eps", ctypes.c_float), ("reserved", _i32),
     ]
 
 

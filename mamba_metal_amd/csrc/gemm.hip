@@ -31,6 +31,13 @@
 //     deterministic, and the kernel boundary orders the partials without any
 //     cross-workgroup protocol.
 //
+// Input RMSNorm (x_norm_w set, M <= 8, linear_kernel only): X holds the raw residual
+// rows; every wave first computes each row's inverse RMS exactly as
+// add_rmsnorm_vec_kernel does (same chunk order, fma chain and shuffle tree), then
+// scales the X operand rows by it and by the norm weight before the LDS write, so the
+// product sees the same rounded operand as after a separate norm pass.  At small batch
+// this drops the norm kernel between out_proj and the next in_proj.
+//
 // Epilogues fold the decode step's neighbouring element-wise ops into the GEMM:
 //   MM_LIN_STORE  y[m, n] = acc
 //   MM_LIN_RESID  resid[m, n] = resid[m, n] + round(acc)     (out_proj + residual,
@@ -52,6 +59,9 @@ constexpr int kMaxM = 64;
 constexpr int kRowBytes = kChunkK * 2 + 16;  // padded LDS row of one X chunk
 constexpr int kXLds = kMaxM * kRowBytes;     // 9216 B per wave for the X chunk
 constexpr int kPartial = 4;                  // internal "epilogue": write fp32 partials
+constexpr int kShareTiles = 512;             // wider N runs the shared-X kernel
+constexpr int kNormInMaxM = 8;               // input RMSNorm: rows of X load instruction 0
+constexpr int kNormInMaxK = 4096;            // input RMSNorm: rows add_rmsnorm_vec_kernel takes
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -81,8 +91,9 @@ struct LinParams {
   const void* norm_w;
   void* norm_out;
   float* partials;  // split calls: [ks][M][N] fp32
+  const void* x_norm_w;  // input RMSNorm weight (K,), or null
   int64_t M, N, K, ldx, ldy, ldr, ldc, ldn, n_conv;
-  float eps;
+  float eps, x_eps;
   int32_t ks;       // K splits across workgroups (grid.y)
 };
 
@@ -106,7 +117,7 @@ inline Plan plan(int64_t N, int64_t K) {
   const int64_t nchunks = K / kChunkK;
   Plan p{1, 1, 1, 0};
   const int64_t nt32 = ceil_div(N, kTileN);
-  if (nt32 > 512) {
+  if (nt32 > kShareTiles) {
     p.nw = nt32 <= 1024 ? 4 : 8;
     return p;
   }
@@ -158,9 +169,11 @@ __device__ __forceinline__ void epilogue(const LinParams& p, int64_t m, int64_t 
 // 8*(i/4) + 4*(l/32) + i%4, column l%32.
 __device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
-template <int DT, int KSW, int MT, int NT, int EPI>
+template <int DT, int KSW, int MT, int NT, int EPI, bool NORM = false>
 __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
   using T = typename Ty<DT>::T;
+  using V8 = typename Ty<DT>::V8;
+  static_assert(!NORM || MT == 1, "the input RMSNorm covers rows 0..7 of one m-tile");
   constexpr int XI = MT * 4;                 // X load instructions per chunk (8 rows each)
   constexpr int NACC = MT * NT * 16;         // accumulator floats per lane
   constexpr int kWaveLds = kXLds > NACC * 64 * 4 ? kXLds : NACC * 64 * 4;
@@ -202,6 +215,33 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
   // LDS slots: write (row 8i + l/8, 16-byte column l%8); read for step g, m-tile mt:
   // row 32mt + l%32, column 2g + l/32.
   const int wr_off = (lane >> 3) * kRowBytes + (lane & 7) * 16;
+
+  // Input RMSNorm: inverse RMS of row l/8 (the rows of X load instruction 0; the host
+  // guarantees M <= 8), computed per row by the whole wave in add_rmsnorm_vec_kernel's
+  // order: lane takes 8-element chunks lane + 64 i, squares accumulate by fma in (i, k)
+  // order, then the xor-shuffle tree 32, 16, ..., 1.  Run after the first chunk's
+  // loads are issued, so the two latencies overlap.
+  float xinv = 0.0f;
+  auto input_norm = [&]() __attribute__((always_inline)) {
+    const int nch = static_cast<int>(p.K >> 3);
+    for (int64_t m = 0; m < p.M; ++m) {
+      const T* const r = static_cast<const T*>(p.x) + m * p.ldx;
+      float ss = 0.0f;
+      for (int i = 0; 64 * i < nch; ++i) {
+        const bool ok = lane + 64 * i < nch;
+        const V8 v = *reinterpret_cast<const V8*>(r + 8 * (ok ? lane + 64 * i : 0));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float x = ok ? Ty<DT>::f(v[k]) : 0.0f;
+          ss = __builtin_fmaf(x, x, ss);
+        }
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      const float inv = rsqrtf(ss / static_cast<float>(p.K) + p.x_eps);
+      if ((lane >> 3) == m) xinv = inv;
+    }
+  };
   const int rd_off = (lane & 31) * kRowBytes + (lane >> 5) * 16;
 
   // Epilogue ownership (reduced tile element e = row * TN + col, e = tid + u * KSW * 64):
@@ -242,7 +282,8 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
   if (c_begin < c_end) {
     const int64_t c_last = c_end - 1;
     u32x4 wa[NT][kSteps], xa[XI], wb[NT][kSteps], xb[XI];
-    auto load = [&](u32x4(&wv)[NT][kSteps], u32x4(&xv)[XI], int64_t c) {
+    u32x4 na = {0u, 0u, 0u, 0u}, nb = na;  // input-norm weight chunk (NORM)
+    auto load = [&](u32x4(&wv)[NT][kSteps], u32x4(&xv)[XI], u32x4& nv, int64_t c) {
       const int64_t cc = c < c_end ? c : c_last;
 #pragma unroll
       for (int j = 0; j < NT; ++j)
@@ -250,12 +291,28 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
         for (int g = 0; g < kSteps; ++g) wv[j][g] = wp[j][(cc * kSteps + g) * 64];
 #pragma unroll
       for (int i = 0; i < XI; ++i) xv[i] = *reinterpret_cast<const u32x4*>(xrow[i] + cc * kChunkK);
+      if constexpr (NORM)
+        nv = *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.x_norm_w) + cc * kChunkK +
+                                             8 * (lane & 7));
     };
-    auto compute = [&](const u32x4(&wv)[NT][kSteps], const u32x4(&xv)[XI], int64_t c) {
+    auto compute = [&](const u32x4(&wv)[NT][kSteps], const u32x4(&xv)[XI], const u32x4& nv,
+                       int64_t c) {
       if (c >= c_end) return;
 #pragma unroll
-      for (int i = 0; i < XI; ++i)
-        *reinterpret_cast<u32x4*>(xs + 8 * i * kRowBytes + wr_off) = xv[i];
+      for (int i = 0; i < XI; ++i) {
+        u32x4 v = xv[i];
+        if constexpr (NORM) {
+          if (i == 0) {  // rows 0..7: round(x * inv * w), add_rmsnorm_vec_kernel's expression
+            const V8 xr = __builtin_bit_cast(V8, v);
+            const V8 wr = __builtin_bit_cast(V8, nv);
+            V8 o;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) o[k] = Ty<DT>::from(Ty<DT>::f(xr[k]) * xinv * Ty<DT>::f(wr[k]));
+            v = __builtin_bit_cast(u32x4, o);
+          }
+        }
+        *reinterpret_cast<u32x4*>(xs + 8 * i * kRowBytes + wr_off) = v;
+      }
       // LDS is in order per wave: the reads below see the writes above; this only
       // keeps the compiler from moving them across.
       __builtin_amdgcn_wave_barrier();
@@ -270,12 +327,13 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
       __builtin_amdgcn_wave_barrier();
     };
 
-    load(wa, xa, c_begin);
+    load(wa, xa, na, c_begin);
+    if constexpr (NORM) input_norm();
     for (int64_t c = c_begin; c < c_end; c += 2) {
-      load(wb, xb, c + 1);
-      compute(wa, xa, c);
-      load(wa, xa, c + 2);
-      compute(wb, xb, c + 1);
+      load(wb, xb, nb, c + 1);
+      compute(wa, xa, na, c);
+      load(wa, xa, na, c + 2);
+      compute(wb, xb, nb, c + 1);
     }
   }
 
@@ -649,23 +707,35 @@ __global__ __launch_bounds__(256) void pack_kernel(const void* __restrict__ w, u
   dst[i] = v;
 }
 
-template <int DT, int KSW, int MT, int NT>
-void launch_epi(const LinParams& p, int32_t epi, dim3 grid, hipStream_t s) {
+template <int DT, int KSW, int MT, int NT, bool NORM>
+void launch_epi_n(const LinParams& p, int32_t epi, dim3 grid, hipStream_t s) {
   const dim3 block(KSW * 64);
   switch (epi) {
     case MM_LIN_STORE:
-      hipLaunchKernelGGL((linear_kernel<DT, KSW, MT, NT, MM_LIN_STORE>), grid, block, 0, s, p);
+      hipLaunchKernelGGL((linear_kernel<DT, KSW, MT, NT, MM_LIN_STORE, NORM>), grid, block, 0, s, p);
       break;
     case MM_LIN_RESID:
-      hipLaunchKernelGGL((linear_kernel<DT, KSW, MT, NT, MM_LIN_RESID>), grid, block, 0, s, p);
+      hipLaunchKernelGGL((linear_kernel<DT, KSW, MT, NT, MM_LIN_RESID, NORM>), grid, block, 0, s, p);
       break;
     case MM_LIN_CONV:
-      hipLaunchKernelGGL((linear_kernel<DT, KSW, MT, NT, MM_LIN_CONV>), grid, block, 0, s, p);
+      hipLaunchKernelGGL((linear_kernel<DT, KSW, MT, NT, MM_LIN_CONV, NORM>), grid, block, 0, s, p);
       break;
     default:
-      hipLaunchKernelGGL((linear_kernel<DT, 1, MT, NT, kPartial>), grid, dim3(64), 0, s, p);
+      hipLaunchKernelGGL((linear_kernel<DT, 1, MT, NT, kPartial, NORM>), grid, dim3(64), 0, s, p);
       break;
   }
+}
+
+// The input-norm instantiations exist for one m-tile only (M <= 8, checked on the host).
+template <int DT, int KSW, int MT, int NT>
+void launch_epi(const LinParams& p, int32_t epi, dim3 grid, hipStream_t s) {
+  if constexpr (MT == 1) {
+    if (p.x_norm_w) {
+      launch_epi_n<DT, KSW, MT, NT, true>(p, epi, grid, s);
+      return;
+    }
+  }
+  launch_epi_n<DT, KSW, MT, NT, false>(p, epi, grid, s);
 }
 
 template <int DT, int MT, int NT>
@@ -842,6 +912,17 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
     if (!aligned(q.conv_state, 8) || !aligned(q.conv_w, 8))
       return fail(MM_ERR_LAYOUT, "conv_state and conv_w must be 8-byte aligned");
   }
+  if (q.reserved != 0) return fail(MM_ERR_LAYOUT, "reserved field must be 0");
+  if (q.x_norm_w) {
+    if (q.M > kNormInMaxM)
+      return fail(MM_ERR_SHAPE, "the input RMSNorm takes M <= %d (M=%lld)", kNormInMaxM, (long long)q.M);
+    if (q.K > kNormInMaxK)
+      return fail(MM_ERR_SHAPE, "the input RMSNorm takes K <= %d", kNormInMaxK);
+    if (ceil_div(q.N, kTileN) > kShareTiles)
+      return fail(MM_ERR_SHAPE, "the input RMSNorm takes N <= %d", kShareTiles * kTileN);
+    if (!aligned(q.x_norm_w, 16)) return fail(MM_ERR_LAYOUT, "x_norm_w must be 16-byte aligned");
+    if (!(q.x_eps >= 0.0f)) return fail(MM_ERR_SHAPE, "x_eps must be >= 0");
+  }
   if (q.M == 0 || q.N == 0) return MM_OK;
   const Plan pl = plan(q.N, q.K);
   const size_t need = mm_decode_linear_workspace_size(q.M, q.N, q.K);
@@ -865,6 +946,8 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
   p.ldn = q.ldn;
   p.eps = q.eps;
   p.partials = need ? static_cast<float*>(q.workspace) : nullptr;
+  p.x_norm_w = q.x_norm_w;
+  p.x_eps = q.x_eps;
   p.M = q.M;
   p.N = q.N;
   p.K = q.K;

@@ -17,6 +17,11 @@ neighbouring element-wise ops folded into its epilogue:
 ``decode_linear_ok`` says whether a call fits the kernel (f16/bf16, M <= 64,
 16-byte aligned rows, K % 64 == 0); callers use torch's GEMM otherwise.
 
+``x_norm=(norm_w, eps)`` (``decode_linear`` and ``decode_in_proj_conv``, M <= 8,
+K <= 4096, N <= 16384, see ``norm_in_ok``): x holds raw residual rows and the product uses
+RMSNorm(x) * norm_w -- the residual block's pre-norm (mamba_model.py:57) -- computed
+in the operand load, bit-identical to ``add_rmsnorm``'s output.
+
 The kernel reads W in a packed operand order: ``packed_weight(w)`` makes that copy
 once per weight (kept while the weight lives and is unchanged -- it doubles the
 decode weights' HBM footprint, 5.6 GB for Mamba-2.8B of 288 GB).  Narrow-N calls
@@ -36,6 +41,9 @@ from mamba_metal_amd import _lib
 LIN_STORE, LIN_RESID, LIN_CONV, LIN_RESID_NORM = 0, 1, 2, 3
 MAX_M = 64
 K_MULTIPLE = 64
+NORM_IN_MAX_M = 8
+NORM_IN_MAX_K = 4096
+NORM_IN_MAX_N = 512 * 32
 _WS_MIN = 8 << 20
 
 _PACKED: dict = {}    # id(w) -> (weakref to w, w._version, w.data_ptr(), packed copy)
@@ -105,7 +113,21 @@ def _call(prm: _lib.LinearParams, dev) -> None:
     _lib.check(st, "mm_decode_linear")
 
 
-def _base(x, w, epi) -> _lib.LinearParams:
+def split_k(M: int, w: torch.Tensor) -> bool:
+    """Whether mm_decode_linear splits K over workgroups for (M, w) -- then a
+    RESID_NORM epilogue runs the norm inside its ordered reduce."""
+    return _lib.load().mm_decode_linear_workspace_size(M, w.shape[0], w.shape[1]) > 0
+
+
+def norm_in_ok(x: torch.Tensor, w: torch.Tensor, norm_w: torch.Tensor) -> bool:
+    """Whether the input RMSNorm can be folded into this call's operand load."""
+    return (decode_linear_ok(x, w) and x.shape[0] <= NORM_IN_MAX_M and w.shape[0] <= NORM_IN_MAX_N
+            and x.shape[1] <= NORM_IN_MAX_K
+            and norm_w.dtype == x.dtype and norm_w.is_contiguous() and norm_w.dim() == 1
+            and norm_w.shape[0] == x.shape[1] and norm_w.data_ptr() % 16 == 0)
+
+
+def _base(x, w, epi, x_norm=None) -> _lib.LinearParams:
     if not decode_linear_ok(x, w):
         raise ValueError("decode_linear: x (M<=64, K) and w (N, K) must be f16/bf16 of one "
                          "dtype with unit inner stride, 16-byte aligned rows and K % 64 == 0")
@@ -115,13 +137,22 @@ def _base(x, w, epi) -> _lib.LinearParams:
     prm.ldx = x.stride(0)
     prm.dtype = _lib.dtype_code(x.dtype)
     prm.epilogue = epi
+    if x_norm is not None:
+        norm_w, eps = x_norm
+        _lib.require_cuda(x, norm_w)
+        if not norm_in_ok(x, w, norm_w):
+            raise ValueError("x_norm: needs M <= 8, K <= 4096, N <= 16384 and a contiguous, 16-byte "
+                             "aligned (K,) weight in x's dtype")
+        prm.x_norm_w, prm.x_eps = norm_w.data_ptr(), float(eps)
     return prm
 
 
-def decode_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None):
-    """y (M, N) = x (M, K) @ w (N, K).T"""
+def decode_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None,
+                  x_norm=None):
+    """y (M, N) = x (M, K) @ w (N, K).T  (x replaced by RMSNorm(x) * norm_w when
+    x_norm = (norm_w, eps) is given)."""
     dev = _lib.require_cuda(x, w, out)
-    prm = _base(x, w, LIN_STORE)
+    prm = _base(x, w, LIN_STORE, x_norm)
     if out is None:
         out = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=dev)
     if out.shape != (x.shape[0], w.shape[0]) or out.stride(1) != 1 or out.dtype != x.dtype:
@@ -169,14 +200,15 @@ def in_proj_conv_ok(x, w, conv_state, conv_w, conv_b) -> bool:
             and conv_state.data_ptr() % 8 == 0 and conv_w.data_ptr() % 8 == 0)
 
 
-def decode_in_proj_conv(x, w, conv_state, conv_w, conv_b=None):
+def decode_in_proj_conv(x, w, conv_state, conv_w, conv_b=None, x_norm=None):
     """in_proj + decode conv-window step.  x (M, K); w (N, K) with N = n_conv + n_z;
     conv_state (M, n_conv, 4) updated in place; conv_w (n_conv, 1, 4) or (n_conv, 4).
+    With x_norm = (norm_w, eps), x is replaced by RMSNorm(x) * norm_w.
     Returns (x_conv (M, n_conv) = silu(conv), z (M, n_z))."""
     dev = _lib.require_cuda(x, w, conv_state, conv_w, conv_b)
     if not in_proj_conv_ok(x, w, conv_state, conv_w, conv_b):
         raise ValueError("decode_in_proj_conv: unsupported layout (see in_proj_conv_ok)")
-    prm = _base(x, w, LIN_CONV)
+    prm = _base(x, w, LIN_CONV, x_norm)
     M, N = x.shape[0], w.shape[0]
     n_conv = conv_state.shape[1]
     x_conv = torch.empty((M, n_conv), dtype=x.dtype, device=dev)

@@ -31,10 +31,15 @@ import torch.nn.functional as F
 
 from mamba_metal_amd.conv1d import causal_conv1d, conv_step
 from mamba_metal_amd.decode import ssm_step_dtproj
-from mamba_metal_amd.linear import (decode_in_proj_conv, decode_linear, decode_linear_ok,
-                                    decode_linear_resid_, decode_linear_resid_norm_,
-                                    in_proj_conv_ok)
+from mamba_metal_amd.linear import (NORM_IN_MAX_M, decode_in_proj_conv, decode_linear,
+                                    decode_linear_ok, decode_linear_resid_,
+                                    decode_linear_resid_norm_, in_proj_conv_ok, norm_in_ok,
+                                    split_k)
+from mamba_metal_amd.norm import add_rmsnorm
 from mamba_metal_amd.selective_scan import selective_scan_into
+
+# step_2d's marker for "resid updated, next norm not applied yet" (see step_2d).
+NORM_PENDING = object()
 
 
 class MambaBlock(nn.Module):
@@ -127,7 +132,8 @@ class MambaBlock(nn.Module):
             conv_state, ssm_state
 
     def step_2d(self, x: torch.Tensor, conv_state: torch.Tensor, ssm_state: torch.Tensor,
-                resid: torch.Tensor | None = None, next_norm: nn.Module | None = None):
+                resid: torch.Tensor | None = None, next_norm: nn.Module | None = None,
+                x_norm: nn.Module | None = None, defer_norm: bool = False):
         """The decode step on a (B, d_model) row block, states updated in place.
 
         in_proj GEMM + conv-window step -> x_proj GEMM -> fused dt_proj + softplus +
@@ -139,12 +145,24 @@ class MambaBlock(nn.Module):
         Without ``resid`` returns out_proj(y).  With ``resid`` returns a pair: ``(y,
         None)`` when the caller still has to add y; ``(None, None)`` when ``resid``
         already holds x + out_proj(y); ``(None, h)`` when in addition h =
-        next_norm(resid)."""
+        next_norm(resid); with ``defer_norm``, ``(None, NORM_PENDING)`` when ``resid``
+        holds x + out_proj(y) and next_norm is left to the next in_proj.
+
+        ``x_norm`` (an RMSNorm): x holds the raw residual rows and the block's input is
+        x_norm(x) -- folded into in_proj's operand load at small batch (bit-identical
+        to the separate norm), applied by ``add_rmsnorm`` first otherwise."""
         di = self.d_inner
         W_in = self.in_proj.weight
-        if in_proj_conv_ok(x, W_in, conv_state, self.conv1d.weight, self.conv1d.bias):
+        conv_ok = in_proj_conv_ok(x, W_in, conv_state, self.conv1d.weight, self.conv1d.bias)
+        fold = None
+        if x_norm is not None:
+            if conv_ok and norm_in_ok(x, W_in, x_norm.weight):
+                fold = (x_norm.weight, x_norm.eps)
+            else:
+                x = add_rmsnorm(x, None, x_norm.weight, x_norm.eps)
+        if conv_ok:
             x_conv, z = decode_in_proj_conv(x, W_in, conv_state, self.conv1d.weight,
-                                            self.conv1d.bias)
+                                            self.conv1d.bias, x_norm=fold)
         else:
             xz = self.in_proj(x)                               # (B, 2*d_inner)
             x_main, z = xz[:, :di], xz[:, di:]
@@ -162,6 +180,10 @@ class MambaBlock(nn.Module):
         if not (fused and resid.dtype == y.dtype and resid.stride(-1) == 1):
             return self.out_proj(y), None
         if next_norm is not None and next_norm.weight.dtype == y.dtype:
+            if defer_norm and y.shape[0] <= NORM_IN_MAX_M and not split_k(y.shape[0], W_out):
+                # no split-K reduce to carry the norm: leave it to the next in_proj
+                decode_linear_resid_(resid, y, W_out)
+                return None, NORM_PENDING
             return None, decode_linear_resid_norm_(resid, y, W_out, next_norm.weight, next_norm.eps)
         decode_linear_resid_(resid, y, W_out)
         return None, None

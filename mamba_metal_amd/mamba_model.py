@@ -15,7 +15,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from mamba_metal_amd.mamba_block import MambaBlock
+from mamba_metal_amd.mamba_block import NORM_PENDING, MambaBlock
 from mamba_metal_amd.linear import decode_linear, decode_linear_ok
 from mamba_metal_amd.norm import add_rmsnorm
 
@@ -77,24 +77,30 @@ class MambaModel(nn.Module):
             return decode_linear(h, E)
         return F.linear(h, E)
 
-    def _run(self, input_ids, mix):
+    def _run(self, input_ids, mix, defer_norm: bool = False):
         """Layer chain with the residual add fused into the next layer's RMSNorm:
         resid += y_prev; h = RMSNorm(resid) (one kernel per layer boundary).
-        ``mix(mixer, h, resid, next_norm)`` returns either ``(y, None)`` -- the mixer
-        output, added here -- or ``(None, h_next)`` when it has already added its
-        output into ``resid`` and applied ``next_norm`` itself."""
+        ``mix(mixer, h, resid, norm, next_norm)`` returns either ``(y, None)`` -- the
+        mixer output, added here -- or ``(None, h_next)`` when it has already added its
+        output into ``resid`` and applied ``next_norm`` itself.  With ``defer_norm`` the
+        first norm is not applied here (h = NORM_PENDING: the mixer applies ``norm`` to
+        ``resid`` itself, in its first projection), and a mixer may return
+        ``(None, NORM_PENDING)`` to leave ``next_norm`` to the next one."""
         resid = self.embeddings(input_ids)
         norms = [layer.norm for layer in self.layers] + [self.norm_f]
-        h = add_rmsnorm(resid, None, norms[0].weight, norms[0].eps)
+        h = NORM_PENDING if defer_norm else add_rmsnorm(resid, None, norms[0].weight,
+                                                        norms[0].eps)
         for i, layer in enumerate(self.layers):
-            y, h_next = mix(layer.mixer, h, resid, norms[i + 1])
+            y, h_next = mix(layer.mixer, h, resid, norms[i], norms[i + 1])
             h = h_next if h_next is not None else add_rmsnorm(resid, y, norms[i + 1].weight,
                                                               norms[i + 1].eps)
+        if h is NORM_PENDING:
+            h = add_rmsnorm(resid, None, norms[-1].weight, norms[-1].eps)
         return h
 
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
         """input_ids (B, L) -> logits (B, L, vocab_size)."""
-        return self._head(self._run(input_ids, lambda m, h, resid, nrm: (m(h), None)))
+        return self._head(self._run(input_ids, lambda m, h, resid, nrm, nxt: (m(h), None)))
 
     def init_state(self, batch_size: int = 1):
         """Zero conv and SSM states (float32, as mamba_model.py:80-91)."""
@@ -112,7 +118,7 @@ class MambaModel(nn.Module):
         conv_states, ssm_states)."""
         convs, ssms = [], []
 
-        def mix(m, h, resid, nrm):
+        def mix(m, h, resid, nrm, nxt):
             y, cs, ss = m.prefill(h)
             convs.append(cs)
             ssms.append(ss)
@@ -132,11 +138,14 @@ class MambaModel(nn.Module):
             ssm_states = [t.clone() for t in ssm_states]
         it = iter(zip(conv_states, ssm_states))
 
-        def mix(m, h, resid, nrm):
+        def mix(m, h, resid, nrm, nxt):
             cs, ss = next(it)
-            return m.step_2d(h, cs, ss, resid=resid, next_norm=nrm)
+            if h is NORM_PENDING:
+                return m.step_2d(resid, cs, ss, resid=resid, next_norm=nxt, x_norm=nrm,
+                                 defer_norm=True)
+            return m.step_2d(h, cs, ss, resid=resid, next_norm=nxt, defer_norm=True)
 
-        h = self._run(input_ids.reshape(-1), mix)
+        h = self._run(input_ids.reshape(-1), mix, defer_norm=True)
         return self._head(h)[:, None, :], list(conv_states), list(ssm_states)
 
 

@@ -48,7 +48,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_version_and_status_names(lib):
-    assert lib.mm_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.mm_abi_version() == _lib.ABI_VERSION == 2
     assert lib.mm_status_name(0) == b"MM_OK"
     assert lib.mm_status_name(-3) == b"MM_ERR_DSTATE"
     assert lib.mm_status_name(-99) == b"MM_ERR_UNKNOWN"
@@ -192,6 +192,14 @@ def test_decode_linear_validation(lib):
     assert call(epilogue=1) == _lib.ERR_NULL_POINTER          # RESID without resid
     assert call(epilogue=2, n_conv=16) == _lib.ERR_NULL_POINTER
     assert call(M=0) == _lib.OK and call(N=0) == _lib.OK
+    # input RMSNorm: M <= 8, N <= 16384, aligned weight, eps >= 0; reserved must be 0
+    assert call(x_norm_w=FAKE, M=9) == _lib.ERR_SHAPE
+    assert call(x_norm_w=FAKE, N=16385) == _lib.ERR_SHAPE
+    assert call(x_norm_w=FAKE, K=4160, ldx=4160) == _lib.ERR_SHAPE
+    assert call(x_norm_w=FAKE + 8) == _lib.ERR_LAYOUT
+    assert call(x_norm_w=FAKE, x_eps=-1.0) == _lib.ERR_SHAPE
+    assert call(x_norm_w=FAKE, M=0) == _lib.OK
+    assert call(reserved=1) == _lib.ERR_LAYOUT
     # narrow N splits K across workgroups: needs a workspace
     need = lib.mm_decode_linear_workspace_size(64, 192, 5120)
     assert need > 0

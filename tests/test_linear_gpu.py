@@ -172,3 +172,59 @@ def test_decode_in_proj_conv(dev, K, di, M, dtype):
     # an input that lands on a rounding boundary may differ by one ulp of dtype
     assert_close(x_conv.float().cpu().numpy(), ref, tol * 4, tol * 4, "x_conv")
     assert_close(st.float().cpu().numpy(), ref_st, tol, tol * 4, "conv state")
+
+
+# Input RMSNorm folded into the operand load: the product must be bit-identical to the
+# separate add_rmsnorm + GEMM (the kernel recomputes the norm in add_rmsnorm's order).
+# Shapes: 130M in_proj (conv) at M = 1, 3, 8; 2.8B in_proj (two tiles per wave); a
+# split-K store (narrow N, K = 4096: the longest row add_rmsnorm's vector kernel takes,
+# 8 chunks per lane); a K whose chunk count is not a multiple of 64 lanes' worth
+# (K = 576: 72 chunks of 8).
+@pytest.mark.parametrize("M,K,N,conv", [(1, 768, 3072, True), (3, 768, 3072, True),
+                                        (8, 768, 3072, True), (1, 2560, 10240, True),
+                                        (2, 4096, 192, False), (8, 576, 300, False)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_input_rmsnorm_matches_separate_norm(dev, M, K, N, conv, dtype):
+    from mamba_metal_amd.linear import decode_in_proj_conv, decode_linear, norm_in_ok
+    from mamba_metal_amd.norm import add_rmsnorm
+
+    g = torch.Generator(device=dev).manual_seed(M * 11 + K + N)
+    resid = (torch.randn((M, K), generator=g, device=dev) * 3.0).to(dtype)
+    nw = (1.0 + 0.1 * torch.randn((K,), generator=g, device=dev)).to(dtype)
+    w = (torch.randn((N, K), generator=g, device=dev) * 0.05).to(dtype)
+    eps = 1e-5
+    assert norm_in_ok(resid, w, nw)
+    h = add_rmsnorm(resid, None, nw, eps)
+    if conv:
+        n_conv = N // 2
+        st0 = torch.randn((M, n_conv, 4), generator=g, device=dev).to(dtype)
+        cw = torch.randn((n_conv, 1, 4), generator=g, device=dev).to(dtype)
+        cb = torch.randn((n_conv,), generator=g, device=dev).to(dtype)
+        st_a, st_b = st0.clone(), st0.clone()
+        xa, za = decode_in_proj_conv(h, w, st_a, cw, cb)
+        xb, zb = decode_in_proj_conv(resid, w, st_b, cw, cb, x_norm=(nw, eps))
+        torch.cuda.synchronize()
+        assert torch.equal(xa, xb) and torch.equal(za, zb) and torch.equal(st_a, st_b)
+    else:
+        ya = decode_linear(h, w)
+        yb = decode_linear(resid, w, x_norm=(nw, eps))
+        torch.cuda.synchronize()
+        assert torch.equal(ya, yb)
+        _check(yb, _ref(h, w), dtype, f"norm-in M={M} K={K} N={N}")
+    # the residual rows are read, not written
+    assert torch.equal(resid, (torch.randn((M, K), generator=torch.Generator(device=dev)
+                                           .manual_seed(M * 11 + K + N), device=dev) * 3.0).to(dtype))
+
+
+def test_input_rmsnorm_rejects_large_m(dev):
+    from mamba_metal_amd.linear import decode_linear, norm_in_ok
+
+    x = torch.randn((9, 256), device=dev).half()
+    w = torch.randn((64, 256), device=dev).half()
+    nw = torch.ones(256, device=dev).half()
+    assert not norm_in_ok(x, w, nw)
+    with pytest.raises(ValueError):
+        decode_linear(x, w, x_norm=(nw, 1e-5))
+    x8 = torch.randn((8, 4160), device=dev).half()      # K beyond the vector norm's rows
+    w8 = torch.randn((64, 4160), device=dev).half()
+    assert not norm_in_ok(x8, w8, torch.ones(4160, device=dev).half())
