@@ -38,6 +38,21 @@ def _common_dtype(*ts):
     return torch.float32
 
 
+_LAST_WS: dict = {}   # device -> workspace of the last call (holds its status word)
+
+
+def scan_status(device=None) -> int:
+    """Status word of the last scan on ``device`` (synchronises that device): 0 when
+    every time segment received its predecessor's carried state; nonzero when a bounded
+    hand-off wait gave up (not expected to happen), i.e. that call's y is not valid."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    ws = _LAST_WS.get(dev)
+    if ws is None:
+        return 0
+    torch.cuda.synchronize(dev)
+    return int(ws[4:8].view(torch.int32).item())
+
+
 def selective_scan_into(u, delta, A, B, C, y, *, D=None, z=None, delta_softplus=False,
                         state_out=None):
     """Run the scan writing into a caller-provided y (any strides, shape of u).
@@ -65,6 +80,7 @@ def selective_scan_into(u, delta, A, B, C, y, *, D=None, z=None, delta_softplus=
 
     ws_bytes = lib.mm_selective_scan_workspace_size(batch, dim, dstate, seqlen)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
+    _LAST_WS[dev] = ws
 
     p = _lib.ScanParams()
     p.u, p.delta, p.A, p.B, p.C = u.data_ptr(), delta.data_ptr(), A.data_ptr(), B.data_ptr(), C.data_ptr()

@@ -251,6 +251,8 @@ def _sampled_parity(oracle_lib, dev, batch, dim, seqlen, n_sample, seed):
     D = torch.ones(dim, device=dev)
     y, h = selective_scan(u, d, A, B, C, D=D, z=z, delta_softplus=True, return_state=True)
     torch.cuda.synchronize()
+    from mamba_metal_amd.selective_scan import scan_status
+    assert scan_status(dev) == 0    # every segment hand-off completed
     rng = np.random.default_rng(seed)
     chans = rng.choice(batch * dim, size=n_sample, replace=False)
     chans = np.unique(np.concatenate([chans, [0, batch * dim - 1]]))
