@@ -6,7 +6,10 @@
 // fp16 vector when channels are contiguous) and a run of TC timesteps; the
 // (width-1)-deep causal window lives in registers and slides along time, so x
 // is read once (plus a (width-1)-step halo per run) and out written once:
-// HBM-bound at ~2 x element size bytes per (b, t, c).
+// HBM-bound at ~2 x element size bytes per (b, t, c).  The run is walked in groups
+// of kU steps whose loads are all issued before any of them is used (clamped to the
+// run's last step, so every load is in bounds and unconditional): one load in flight
+// per thread left the kernel latency-bound at a third of the HBM rate.
 //
 // The decode step replaces mamba_block.py:170-177: shift the (batch, dim, width)
 // window left in place, append x, dot with the taps, add bias, SiLU.
@@ -18,6 +21,7 @@ namespace mm {
 namespace conv {
 
 constexpr int kCV = 8;      // channels per thread
+constexpr int kU = 8;       // timesteps per load group
 constexpr int kMaxW = 8;    // largest width accepted
 constexpr int kBlock = 256;
 
@@ -38,7 +42,7 @@ __device__ __forceinline__ float ld_any(const void* p, int64_t i, int32_t dt) {
 
 // K = compile-time width; K == 0 means "runtime width <= kMaxW" using a zero-padded
 // kMaxW-tap window (taps aligned to the newest input).
-template <int DT, int K>
+template <int DT, int K, bool VEC>
 __global__ __launch_bounds__(kBlock) void conv1d_kernel(const Params p) {
   using T = typename Ty<DT>::T;
   using V8 = typename Ty<DT>::V8;
@@ -66,14 +70,10 @@ __global__ __launch_bounds__(kBlock) void conv1d_kernel(const Params p) {
     bias[j] = (cin && p.bias) ? ld_any(p.bias, c, p.w_dtype) : 0.0f;
   }
 
+  // x[b, t, c0 .. c0 + 7] (t >= 0); channels past dim read as zero.
   auto load_x = [&](int64_t t, float v[kCV]) {
-    if (t < 0) {
-#pragma unroll
-      for (int j = 0; j < kCV; ++j) v[j] = 0.0f;
-      return;
-    }
     const T* xp = static_cast<const T*>(p.x) + b * p.xs0 + t * p.xs1;
-    if (p.vec_ok) {
+    if constexpr (VEC) {
       if (c0 < p.dim) {
         const V8 r = *reinterpret_cast<const V8*>(xp + c0);
 #pragma unroll
@@ -94,11 +94,40 @@ __global__ __launch_bounds__(kBlock) void conv1d_kernel(const Params p) {
   // win[k] holds x[t - (W-1) + k] for k < W-1 (the causal history).
   float win[W > 1 ? W - 1 : 1][kCV];
 #pragma unroll
-  for (int k = 0; k < W - 1; ++k) load_x(t_begin - (W - 1) + k, win[k]);
+  for (int k = 0; k < W - 1; ++k) {
+    const int64_t t = t_begin - (W - 1) + k;
+    if (t >= 0) {
+      load_x(t, win[k]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kCV; ++j) win[k][j] = 0.0f;
+    }
+  }
 
-  float xn[kCV];
-  for (int64_t t = t_begin; t < t_end; ++t) {
-    load_x(t, xn);
+  // Vector path: the group's raw 16-byte rows are loaded before any is converted (every
+  // thread's channel group is inside dim there, so no load is guarded).
+  constexpr int U = VEC ? kU : 1;
+  const T* const xb = static_cast<const T*>(p.x) + b * p.xs0 + c0;
+  for (int64_t t0 = t_begin; t0 < t_end; t0 += U) {
+  V8 xr[U];
+  float xs[VEC ? 1 : kCV];
+  if constexpr (VEC) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      xr[u] = *reinterpret_cast<const V8*>(xb + (t0 + u < t_end ? t0 + u : t_end - 1) * p.xs1);
+  } else {
+    load_x(t0, xs);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t t = t0 + u;
+    if (t >= t_end) break;
+    float xn[kCV];
+#pragma unroll
+    for (int j = 0; j < kCV; ++j) {
+      if constexpr (VEC) xn[j] = Ty<DT>::f(xr[u][j]);
+      else xn[j] = xs[j];
+    }
     float o[kCV];
 #pragma unroll
     for (int j = 0; j < kCV; ++j) {
@@ -109,7 +138,7 @@ __global__ __launch_bounds__(kBlock) void conv1d_kernel(const Params p) {
       o[j] = p.apply_silu ? silu_f(acc) : acc;
     }
     T* op = static_cast<T*>(p.out) + b * p.os0 + t * p.os1;
-    if (p.vec_ok) {
+    if constexpr (VEC) {
       if (c0 < p.dim) {
         V8 r;
 #pragma unroll
@@ -147,19 +176,26 @@ __global__ __launch_bounds__(kBlock) void conv1d_kernel(const Params p) {
       for (int j = 0; j < kCV; ++j) win[W - 2][j] = xn[j];
     }
   }
-
+  }
 }
 
 template <int DT>
 void launch_dt(const Params& p, hipStream_t s) {
   const int64_t total = p.batch * p.nchunks * p.ncg;
   const dim3 grid(static_cast<unsigned>(ceil_div(total, kBlock)));
-  switch (p.width) {
-    case 2: hipLaunchKernelGGL((conv1d_kernel<DT, 2>), grid, dim3(kBlock), 0, s, p); break;
-    case 3: hipLaunchKernelGGL((conv1d_kernel<DT, 3>), grid, dim3(kBlock), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((conv1d_kernel<DT, 4>), grid, dim3(kBlock), 0, s, p); break;
-    default: hipLaunchKernelGGL((conv1d_kernel<DT, 0>), grid, dim3(kBlock), 0, s, p); break;
+#define MM_CONV_W(V)                                                                          \
+  switch (p.width) {                                                                          \
+    case 2: hipLaunchKernelGGL((conv1d_kernel<DT, 2, V>), grid, dim3(kBlock), 0, s, p); break; \
+    case 3: hipLaunchKernelGGL((conv1d_kernel<DT, 3, V>), grid, dim3(kBlock), 0, s, p); break; \
+    case 4: hipLaunchKernelGGL((conv1d_kernel<DT, 4, V>), grid, dim3(kBlock), 0, s, p); break; \
+    default: hipLaunchKernelGGL((conv1d_kernel<DT, 0, V>), grid, dim3(kBlock), 0, s, p); break; \
   }
+  if (p.vec_ok) {
+    MM_CONV_W(true)
+  } else {
+    MM_CONV_W(false)
+  }
+#undef MM_CONV_W
 }
 
 // ---------------------------------------------------------------------------
@@ -281,9 +317,10 @@ int mm_causal_conv1d_fwd(const void* x, const void* weight, const void* bias, vo
                  ? 1
                  : 0;
   p.ncg = ceil_div(dim, kCV);
-  // Run length: enough runs to give >= ~64k threads, runs of at most 256 steps.
+  // Run length: enough runs for >= ~256k threads (~16 waves per CU), runs of at most
+  // 256 steps and at least kU (one load group; the (width-1)-step halo is re-read per run).
   int64_t tc = 256;
-  while (tc > 8 && batch * p.ncg * ceil_div(seqlen, tc) < 65536) tc /= 2;
+  while (tc > kU && batch * p.ncg * ceil_div(seqlen, tc) < 262144) tc /= 2;
   p.tc = tc;
   p.nchunks = ceil_div(seqlen, tc);
 
