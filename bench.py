@@ -184,6 +184,36 @@ def decode_bench(name, cfg_kw, batch, prompt_len, n_decode, seed=0):
     return res
 
 
+def gemm_probe(calls=24, n_weights=12):
+    """The decode GEMM at Mamba-2.8B's in_proj shape (M=64, K=2560, N=10240 fp16), weights
+    rotated so each call streams its 52 MB from HBM; HIP-event average per call."""
+    import torch
+
+    from mamba_metal_amd.linear import decode_linear, packed_weight
+
+    dev = torch.device("cuda:0")
+    M, K, N = 64, 2560, 10240
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    ws = [(torch.randn((N, K), generator=g, device=dev) * 0.02).half() for _ in range(n_weights)]
+    for w in ws:
+        packed_weight(w)
+    x = torch.randn((M, K), generator=g, device=dev).half()
+    out = torch.empty((M, N), device=dev, dtype=torch.float16)
+    for i in range(3):
+        decode_linear(x, ws[i % n_weights], out=out)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(calls):
+        decode_linear(x, ws[i % n_weights], out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / calls
+    return {"gemm": "decode in_proj M=64 K=2560 N=10240 fp16", "us_per_call": us,
+            "weight_gbs": N * K * 2 / us / 1e3, "calls": calls}
+
+
 def decode_roofline_bytes(d_model, n_layer, vocab, d_state, d_conv, dt_rank, batch):
     """Weights (fp16) once + fp32 SSM state r/w + fp16 conv state r/w per decode step."""
     di = 2 * d_model
@@ -210,6 +240,8 @@ def main():
                     help="run one decode benchmark only (the command of the decode profiles)")
     ap.add_argument("--only-scan", action="store_true",
                     help="config-4 scan only (the command the committed rocprof summaries use)")
+    ap.add_argument("--only-gemm", action="store_true",
+                    help="the decode GEMM at the 2.8B in_proj shape only (counter profiles)")
     args = ap.parse_args()
     if args.only_scan:
         args.no_extra = args.no_decode = args.no_cpu = True
@@ -222,6 +254,10 @@ def main():
 
     from mamba_metal_amd import _lib
 
+    if args.only_gemm:
+        _lib.load()
+        print(json.dumps(gemm_probe()))
+        return
     if args.only_decode:
         _lib.load()
         if args.only_decode == "130m":
