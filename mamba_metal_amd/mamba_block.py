@@ -93,7 +93,13 @@ class MambaBlock(nn.Module):
                                conv_state_out=conv_state)      # (B, L, d_inner)
         x_dbl = self.x_proj(x_main)                            # (B, L, dt_rank + 2N)
         dt_pre, Bm, Cm = self._split_xdbl(x_dbl)
-        dt = F.linear(dt_pre, self.dt_proj.weight, self.dt_proj.bias)  # (B, L, d_inner)
+        # dt_proj as one 2-D GEMM on the strided dt slice (leading dims merge into a view
+        # with row stride dt_rank + 2N), bias in the GEMM epilogue: F.linear on the
+        # non-contiguous 3-D slice added the bias in a separate pass over (B, L, d_inner).
+        dt_2d = dt_pre.reshape(Bsz * L, -1)
+        W_dt = self.dt_proj.weight.t()
+        dt = (torch.addmm(self.dt_proj.bias, dt_2d, W_dt) if self.dt_proj.bias is not None
+              else dt_2d @ W_dt).view(Bsz, L, di)
         y = torch.empty_like(x_main)
         selective_scan_into(x_main.transpose(1, 2), dt.transpose(1, 2), self._A(),
                             Bm.transpose(1, 2), Cm.transpose(1, 2), y.transpose(1, 2),
