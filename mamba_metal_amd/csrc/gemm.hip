@@ -307,7 +307,7 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
             const V8 wr = __builtin_bit_cast(V8, nv);
             V8 o;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) o[k] = Ty<DT>::from(Ty<DT>::f(xr[k]) * xinv * Ty<DT>::f(wr[k]));
+            for (int k = 0; k < 8; ++k) o[k] = norm_round<DT>(Ty<DT>::f(xr[k]), xinv, Ty<DT>::f(wr[k]));
             v = __builtin_bit_cast(u32x4, o);
           }
         }
@@ -683,10 +683,162 @@ __global__ __launch_bounds__(256) void reduce_norm_kernel(const LinParams p) {
     if (tid + 256 * u < ng) {
       T4 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = Ty<DT>::from(nv[u][e] * inv * Ty<DT>::f(wv[u][e]));
+      for (int e = 0; e < 4; ++e) o[e] = norm_round<DT>(nv[u][e], inv, Ty<DT>::f(wv[u][e]));
       orow[tid + 256 * u] = o;
     }
   }
+}
+
+// Small-M path (M <= 4): a weight-streaming GEMV.  With one to four rows the 32-row
+// MFMA tile is mostly padding and the kernel is pure weight streaming, whose rate is set
+// per CU (an L1 keeps ~84 L2 reads of 128 bytes in flight, ~40 GB/s): what matters is
+// spreading W evenly over all CUs.  A workgroup owns 8 output columns and all of K.
+// Thread t takes column n0 + t%8, half (t/8)%2 of each 16-wide k step, and steps
+// t/16, t/16 + 16, ...: in the packed layout each 16-thread group reads two contiguous
+// 128-byte pieces per step.  Each thread accumulates in k order in fp32; the 32 threads
+// of a column are combined by an xor-shuffle tree (within a wave) and then in wave
+// order through LDS -- deterministic.  Loads run kGvU steps ahead of their use
+// (clamped to the last step: every load is in bounds and unconditional).  The input
+// RMSNorm (NORM) is computed by wave 0 in add_rmsnorm_vec_kernel's order and applied as
+// each x chunk is loaded, as in linear_kernel.  Epilogues as the split-K reduce.
+constexpr int kGvCols = 8;
+constexpr int kGvThreads = 256;
+constexpr int kGvMaxM = 4;
+constexpr int kGvU = 4;
+
+template <int DT, int MM, int EPI, bool NORM>
+__global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
+  using T = typename Ty<DT>::T;
+  using V8 = typename Ty<DT>::V8;
+  __shared__ float s_red[kGvThreads / 64][MM][kGvCols];
+  __shared__ float s_inv[MM];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int j = tid & 7;
+  const int hk = (tid >> 3) & 1;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * kGvCols + j;
+  const int64_t nc = n < p.N ? n : 0;
+  const int64_t nsteps = p.K / kStepK;
+  const u32x4* const wb = static_cast<const u32x4*>(p.w) + (nc >> 5) * nsteps * 64 + (nc & 31) + 32 * hk;
+  const T* xr[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m)
+    xr[m] = static_cast<const T*>(p.x) + (m < p.M ? m : 0) * p.ldx + 8 * hk;
+
+  if constexpr (NORM) {  // inverse RMS of each row, add_rmsnorm_vec_kernel's order
+    if (wave == 0) {
+      const int nch = static_cast<int>(p.K >> 3);
+      for (int64_t m = 0; m < p.M; ++m) {
+        const T* const r = static_cast<const T*>(p.x) + m * p.ldx;
+        float ss = 0.0f;
+        for (int i = 0; 64 * i < nch; ++i) {
+          const bool ok = lane + 64 * i < nch;
+          const V8 v = *reinterpret_cast<const V8*>(r + 8 * (ok ? lane + 64 * i : 0));
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const float x = ok ? Ty<DT>::f(v[k]) : 0.0f;
+            ss = __builtin_fmaf(x, x, ss);
+          }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if (lane == 0) s_inv[m] = rsqrtf(ss / static_cast<float>(p.K) + p.x_eps);
+      }
+    }
+    __syncthreads();
+  }
+  float xinv[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) xinv[m] = NORM ? s_inv[m < p.M ? m : 0] : 0.0f;
+
+  float acc[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) acc[m] = 0.0f;
+  const int64_t s_last = nsteps - 1;
+  for (int64_t s0 = tid >> 4; s0 < nsteps; s0 += 16 * kGvU) {
+    u32x4 wv[kGvU], nv[kGvU];
+    V8 xv[kGvU][MM];
+#pragma unroll
+    for (int u = 0; u < kGvU; ++u) {
+      const int64_t st = s0 + 16 * u < nsteps ? s0 + 16 * u : s_last;
+      wv[u] = wb[st * 64];
+#pragma unroll
+      for (int m = 0; m < MM; ++m) xv[u][m] = *reinterpret_cast<const V8*>(xr[m] + st * kStepK);
+      if constexpr (NORM)
+        nv[u] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.x_norm_w) + st * kStepK + 8 * hk);
+    }
+    // Steps past the end were loaded (clamped) and count with a zero weight: consuming
+    // every load unconditionally keeps the compiler from sinking them behind a branch.
+#pragma unroll
+    for (int u = 0; u < kGvU; ++u) {
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      const V8 w8 = __builtin_bit_cast(V8, s0 + 16 * u < nsteps ? wv[u] : zero);
+#pragma unroll
+      for (int m = 0; m < MM; ++m) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float x = Ty<DT>::f(xv[u][m][e]);
+          if constexpr (NORM)
+            x = Ty<DT>::f(norm_round<DT>(x, xinv[m], Ty<DT>::f(__builtin_bit_cast(V8, nv[u])[e])));
+          acc[m] = __builtin_fmaf(x, Ty<DT>::f(w8[e]), acc[m]);
+        }
+      }
+    }
+  }
+  // column sums: lanes j, j+8, ..., j+56 of a wave, then the 4 waves in order
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) acc[m] += __shfl_xor(acc[m], off, 64);
+    if (lane < kGvCols) s_red[wave][m][lane] = acc[m];
+  }
+  __syncthreads();
+  if (tid < MM * kGvCols) {
+    const int m = tid / kGvCols, jj = tid % kGvCols;
+    const int64_t nn = static_cast<int64_t>(blockIdx.x) * kGvCols + jj;
+    float v = s_red[0][m][jj];
+#pragma unroll
+    for (int w = 1; w < kGvThreads / 64; ++w) v += s_red[w][m][jj];
+    if (m < p.M && nn < p.N) epilogue<DT, EPI>(p, m, nn, v);
+  }
+}
+
+template <int DT, int MM, bool NORM>
+void launch_gemv_e(const LinParams& p, int32_t epi, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(ceil_div(p.N, kGvCols)));
+  switch (epi) {
+    case MM_LIN_STORE:
+      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_STORE, NORM>), grid, dim3(kGvThreads), 0, s, p);
+      break;
+    case MM_LIN_RESID:
+      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_RESID, NORM>), grid, dim3(kGvThreads), 0, s, p);
+      break;
+    default:
+      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_CONV, NORM>), grid, dim3(kGvThreads), 0, s, p);
+      break;
+  }
+}
+
+template <int DT>
+void launch_gemv(const LinParams& p, int32_t epi, hipStream_t s) {
+  const bool norm = p.x_norm_w != nullptr;
+#define MM_GV(MMV)                                       \
+  if (norm) launch_gemv_e<DT, MMV, true>(p, epi, s);     \
+  else launch_gemv_e<DT, MMV, false>(p, epi, s)
+  if (p.M == 1) {
+    MM_GV(1);
+  } else if (p.M == 2) {
+    MM_GV(2);
+  } else {
+    MM_GV(4);
+  }
+#undef MM_GV
+}
+
+// The GEMV covers M <= 4 where the shared-X kernel would not run (N <= 16384 columns).
+inline bool use_gemv(int64_t M, int64_t N) {
+  return M <= kGvMaxM && ceil_div(N, kTileN) <= kShareTiles;
 }
 
 // Packed layout: dst block (t, s), lane l = W[32t + l%32, 16s + 8(l/32) .. +7]
@@ -874,6 +1026,7 @@ size_t mm_decode_linear_workspace_size(int64_t M, int64_t N, int64_t K) {
   using namespace mm;
   using namespace mm::gemm;
   if (M <= 0 || N <= 0 || K <= 0 || M > kMaxM || K % kChunkK != 0) return 0;
+  if (use_gemv(M, N)) return 0;
   const Plan pl = plan(N, K);
   if (pl.ks == 1) return 0;
   return static_cast<size_t>(pl.ks * M * N * 4);
@@ -956,7 +1109,7 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
   p.ldr = q.ldr;
   p.ldc = q.ldc;
   p.n_conv = q.n_conv;
-  p.ks = pl.ks;
+  p.ks = use_gemv(q.M, q.N) ? 1 : pl.ks;  // the GEMV keeps K in the workgroup
   const dim3 grid(static_cast<unsigned>(ceil_div(q.N, kTileN * (pl.nw > 0 ? pl.nw : pl.nt))),
                   static_cast<unsigned>(pl.ks));
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -964,7 +1117,10 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
   const bool fused_norm = norm && fused_norm_ok(p, q.dtype, q.resid, q.norm_w, q.norm_out);
   const int32_t epi = norm ? MM_LIN_RESID : q.epilogue;  // RESID_NORM = RESID + norm pass
   const int32_t main_epi = pl.ks > 1 ? kPartial : epi;
-  if (pl.nw > 0) {
+  if (use_gemv(q.M, q.N)) {
+    if (q.dtype == MM_F16) launch_gemv<MM_F16>(p, epi, s);
+    else launch_gemv<MM_BF16>(p, epi, s);
+  } else if (pl.nw > 0) {
     if (q.dtype == MM_F16) launch_share<MM_F16>(p, epi, pl, grid, s);
     else launch_share<MM_BF16>(p, epi, pl, grid, s);
   } else if (q.dtype == MM_F16) {

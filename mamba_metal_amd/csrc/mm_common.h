@@ -90,6 +90,19 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 __device__ __forceinline__ float log2_hw(float x) { return __builtin_amdgcn_logf(x); }
 __device__ __forceinline__ float rcp_hw(float x) { return __builtin_amdgcn_rcpf(x); }
 
+// RMSNorm output element: round(x * inv * w) to DT with the fp32 product rounded first.
+// The empty asm makes the fp32 product an opaque register value, so instruction selection
+// cannot fuse the last multiply and the conversion into one single-rounding
+// mixed-precision instruction (v_fma_mixlo_f16, which it otherwise picks in some kernels
+// and not others): every RMSNorm site -- the norm kernels and the GEMMs that normalise
+// their operand on load -- then rounds identically.
+template <int DT>
+__device__ __forceinline__ typename Ty<DT>::T norm_round(float x, float inv, float w) {
+  float t = x * inv * w;
+  asm("" : "+v"(t));
+  return Ty<DT>::from(t);
+}
+
 // silu(z) = z * sigmoid(z) (selective_scan_chunked.metal:143).
 __device__ __forceinline__ float silu_f(float z) { return z * rcp_hw(1.0f + exp2_hw(-z * kLog2e)); }
 

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_vec_kernel(
     if (lane + 64 * i < nch) {
       V8 ov;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) ov[k] = Ty<DT>::from(v[i][k] * inv * Ty<WT>::f(wv[i][k]));
+      for (int k = 0; k < 8; ++k) ov[k] = norm_round<DT>(v[i][k], inv, Ty<WT>::f(wv[i][k]));
       *reinterpret_cast<V8*>(o + 8 * (lane + 64 * i)) = ov;
     }
   }
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(
     if (c < dim) {
       const float w = w_dtype == MM_F32 ? ld<MM_F32>(weight, c)
                       : w_dtype == MM_F16 ? ld<MM_F16>(weight, c) : ld<MM_BF16>(weight, c);
-      o[c] = Ty<DT>::from(v[i] * inv * w);
+      o[c] = norm_round<DT>(v[i], inv, w);
     }
   }
 }
