@@ -98,7 +98,9 @@ def test_decode_linear_strided_rows(dev):
 
 
 # (64, 5120, 2560): 2.8B out_proj (split K); (40, 128, 16600): shared-X kernel, ragged
-@pytest.mark.parametrize("M,K,N", [(64, 5120, 2560), (40, 128, 16600)])
+# (2, 1536, 768) and (4, 5120, 2560): the M <= 4 GEMV path with the RESID epilogue.
+@pytest.mark.parametrize("M,K,N", [(64, 5120, 2560), (40, 128, 16600), (2, 1536, 768),
+                                   (4, 5120, 2560)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_decode_linear_resid(dev, M, K, N, dtype):
     from mamba_metal_amd.linear import decode_linear_resid_
@@ -148,7 +150,7 @@ def test_decode_linear_resid_norm(dev, M, K, N, dtype):
 # di = 1536: 130M shape; di = 5120: 2.8B width (two column tiles per wave); di = 8300
 # (the conv / z boundary inside a 32-column tile): > 512 column tiles, shared-X kernel
 @pytest.mark.parametrize("K,di", [(768, 1536), (256, 5120), (128, 8300)])
-@pytest.mark.parametrize("M", [64, 3])
+@pytest.mark.parametrize("M", [64, 3, 1])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_decode_in_proj_conv(dev, K, di, M, dtype):
     """in_proj + conv-window step == GEMM, then the oracle's decode conv step."""
@@ -228,3 +230,22 @@ def test_input_rmsnorm_rejects_large_m(dev):
     x8 = torch.randn((8, 4160), device=dev).half()      # K beyond the vector norm's rows
     w8 = torch.randn((64, 4160), device=dev).half()
     assert not norm_in_ok(x8, w8, torch.ones(4160, device=dev).half())
+
+
+# The M <= 4 GEMV path (8 output columns per workgroup, all of K): every M it
+# instantiates (1, 2 and 4 rows; 3 runs the 4-row kernel with a clamped row), N not a
+# multiple of 8 (the last workgroup's columns past N are computed on column 0 and not
+# stored), K of one 16-wide step group (64) up to 5120 (several load groups per thread).
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("K,N", [(64, 50), (768, 3072), (5120, 203), (2560, 16384)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_linear_small_m(dev, M, K, N, dtype):
+    from mamba_metal_amd.linear import decode_linear
+
+    g = torch.Generator(device=dev).manual_seed(M * 100 + K + N)
+    x = torch.randn((M, K), generator=g, device=dev).to(dtype)
+    w = (torch.randn((N, K), generator=g, device=dev) * 0.05).to(dtype)
+    y = decode_linear(x, w)
+    torch.cuda.synchronize()
+    _check(y, _ref(x, w), dtype, f"gemv M={M} K={K} N={N}")
+    assert torch.equal(y, decode_linear(x, w))      # deterministic
