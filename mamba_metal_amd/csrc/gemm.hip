@@ -25,11 +25,13 @@
 //     on): with enough tiles (or a small weight share) K stays in the workgroup, its KSW
 //     waves split K and their partial tiles meet in LDS (summed in fixed wave order)
 //     before the epilogue.
-//     Narrow calls split K over the grid's y dimension instead: single-wave
-//     workgroups write fp32 partial tiles, row-major [split][M][N], to the workspace,
-//     and a second kernel sums the splits in order and runs the epilogue --
-//     deterministic, and the kernel boundary orders the partials without any
-//     cross-workgroup protocol.
+//     Narrow calls split K over the grid's y dimension instead: workgroups write fp32
+//     partial tiles, row-major [split][M][N], to the workspace, and a second kernel
+//     sums the splits in order and runs the epilogue -- deterministic, and the kernel
+//     boundary orders the partials without any cross-workgroup protocol.  With >= 16
+//     column tiles the split workgroups are share_kernel's (4 waves sharing X, up to 8
+//     splits); below that, single-wave linear_kernel workgroups;
+//   * M <= 4: gemv_kernel (below), 8 output columns per workgroup over all CUs.
 //
 // Input RMSNorm (x_norm_w set, M <= 8, linear_kernel only): X holds the raw residual
 // rows; every wave first computes each row's inverse RMS exactly as
@@ -126,6 +128,17 @@ inline Plan plan(int64_t N, int64_t K) {
   const int64_t wg_bytes = kTileN * p.nt * K * 2;
   if (ntiles >= 128 || wg_bytes <= (160 << 10)) {
     while (p.ksw < 4 && ntiles * p.ksw < 512 && nchunks / (p.ksw * 2) >= 2) p.ksw *= 2;
+  } else if (nt32 >= 16) {
+    // K split with X shared by 4 waves over 128 columns: single-wave split workgroups
+    // re-read their K range of X once per 32-column tile, which at M = 64 is twice the
+    // weight bytes (2.8B out_proj: 52 MB of X for 26 MB of W); sharing cuts it 4x.
+    // Splits double up to 8 while the grid is under 256 workgroups and each keeps >= 2
+    // chunks.  Measured at the 2.8B out_proj shape (+ residual + norm pass): 8 splits
+    // (160 workgroups of 10 chunks) 14.5 us; 16 splits 18.0; 4 splits 17.7; 8 waves x 8 or
+    // 16 splits 17.9 / 16.6; single-wave 8-way split (640 workgroups) 16.2.
+    p.nw = 4;
+    const int64_t groups = ceil_div(nt32, 4);
+    while (p.ks < 8 && groups * p.ks < 256 && nchunks / (p.ks * 2) >= 2) p.ks *= 2;
   } else {
     while (p.ks < 64 && ntiles * p.ks < 640 && nchunks / (p.ks * 2) >= 2) p.ks *= 2;
   }
@@ -451,7 +464,13 @@ __global__ __launch_bounds__(NW * 64, 1) void share_kernel(const LinParams p) {
   const int wave = threadIdx.x >> 6;
   const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * NW + wave) * kTileN;
   const int64_t nsteps = p.K / kStepK;
-  const int64_t nchunks = p.K / kChunkK;
+  // K range: all of K, or split blockIdx.y of gridDim.y (then the epilogue writes fp32
+  // partials and the ordered reduce pass runs the real epilogue).  A range past the end
+  // is empty: its loads re-read the last chunk and its partial tile is zero.
+  const int64_t kch = p.K / kChunkK;
+  const int64_t per_wg = (kch + gridDim.y - 1) / gridDim.y;
+  const int64_t cbeg = static_cast<int64_t>(blockIdx.y) * per_wg;
+  const int64_t nchunks = cbeg + per_wg < kch ? cbeg + per_wg : kch;  // end of this range
   const int64_t ntiles32 = (p.N + kTileN - 1) / kTileN;
   const int64_t tile = n0 / kTileN < ntiles32 ? n0 / kTileN : 0;
   const u32x4* const wp = static_cast<const u32x4*>(p.w) + tile * nsteps * 64 + lane;
@@ -523,9 +542,9 @@ __global__ __launch_bounds__(NW * 64, 1) void share_kernel(const LinParams p) {
       }
   };
   S s0, s1, s2;
-  load(s0, 0);
-  load(s1, 1);
-  for (int64_t c = 0; c < nchunks; c += 3) {
+  load(s0, cbeg);
+  load(s1, cbeg + 1);
+  for (int64_t c = cbeg; c < nchunks; c += 3) {
     load(s2, c + 2);
     compute(s0, c, 0);
     load(s0, c + 3);
@@ -535,7 +554,16 @@ __global__ __launch_bounds__(NW * 64, 1) void share_kernel(const LinParams p) {
   }
 
   // ---- epilogue: lane holds column n0 + l % 32, rows 32 mt + acc_row(i, l) ----
-  if constexpr (EPI == MM_LIN_STORE) {
+  if constexpr (EPI == kPartial) {
+    float* const dst = p.partials + static_cast<int64_t>(blockIdx.y) * p.M * p.N;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t m = 32 * mt + acc_row(i, lane);
+        if (ncol && m < p.M) dst[m * p.N + n] = acc[mt][i];
+      }
+  } else if constexpr (EPI == MM_LIN_STORE) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -912,6 +940,9 @@ template <int DT, int NW, int MT>
 void launch_share_epi(const LinParams& p, int32_t epi, dim3 grid, hipStream_t s) {
   const dim3 block(NW * 64);
   switch (epi) {
+    case kPartial:
+      hipLaunchKernelGGL((share_kernel<DT, NW, MT, kPartial>), grid, block, 0, s, p);
+      break;
     case MM_LIN_STORE:
       hipLaunchKernelGGL((share_kernel<DT, NW, MT, MM_LIN_STORE>), grid, block, 0, s, p);
       break;
@@ -1121,8 +1152,15 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
     if (q.dtype == MM_F16) launch_gemv<MM_F16>(p, epi, s);
     else launch_gemv<MM_BF16>(p, epi, s);
   } else if (pl.nw > 0) {
-    if (q.dtype == MM_F16) launch_share<MM_F16>(p, epi, pl, grid, s);
-    else launch_share<MM_BF16>(p, epi, pl, grid, s);
+    if (q.dtype == MM_F16) {
+      launch_share<MM_F16>(p, main_epi, pl, grid, s);
+      if (fused_norm) launch_reduce_norm<MM_F16>(p, s);
+      else if (pl.ks > 1) launch_reduce<MM_F16>(p, epi, s);
+    } else {
+      launch_share<MM_BF16>(p, main_epi, pl, grid, s);
+      if (fused_norm) launch_reduce_norm<MM_BF16>(p, s);
+      else if (pl.ks > 1) launch_reduce<MM_BF16>(p, epi, s);
+    }
   } else if (q.dtype == MM_F16) {
     launch_main<MM_F16>(p, main_epi, pl, grid, s);
     if (fused_norm) launch_reduce_norm<MM_F16>(p, s);
