@@ -178,6 +178,35 @@ __device__ __forceinline__ void epilogue(const LinParams& p, int64_t m, int64_t 
   }
 }
 
+// One lane's part of a row's sum of squares in add_rmsnorm_vec_kernel's order: lane
+// takes 8-element chunks lane + 64 i (i < kNormChunks: rows of up to 4096 elements),
+// squares accumulated by fma in (i, k) order, chunks past the row counted as zeros.  All
+// chunk loads are issued (clamped to chunk 0) before the first is used.
+constexpr int kNormChunks = 8;
+static_assert(kNormChunks * 64 * 8 == kNormInMaxK, "row_sumsq covers rows of kNormInMaxK elements");
+
+template <int DT>
+__device__ __forceinline__ float row_sumsq(const typename Ty<DT>::T* r, int nch, int lane) {
+  using V8 = typename Ty<DT>::V8;
+  V8 v[kNormChunks];
+#pragma unroll
+  for (int i = 0; i < kNormChunks; ++i) {
+    const int ch = lane + 64 * i;
+    v[i] = *reinterpret_cast<const V8*>(r + 8 * (ch < nch ? ch : 0));
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormChunks; ++i) {
+    const bool ok = lane + 64 * i < nch;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float x = ok ? Ty<DT>::f(v[i][k]) : 0.0f;
+      ss = __builtin_fmaf(x, x, ss);
+    }
+  }
+  return ss;
+}
+
 // MFMA output layout: lane l, register i of a 32x32 tile holds row
 // 8*(i/4) + 4*(l/32) + i%4, column l%32.
 __device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
@@ -239,16 +268,7 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
     const int nch = static_cast<int>(p.K >> 3);
     for (int64_t m = 0; m < p.M; ++m) {
       const T* const r = static_cast<const T*>(p.x) + m * p.ldx;
-      float ss = 0.0f;
-      for (int i = 0; 64 * i < nch; ++i) {
-        const bool ok = lane + 64 * i < nch;
-        const V8 v = *reinterpret_cast<const V8*>(r + 8 * (ok ? lane + 64 * i : 0));
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const float x = ok ? Ty<DT>::f(v[k]) : 0.0f;
-          ss = __builtin_fmaf(x, x, ss);
-        }
-      }
+      float ss = row_sumsq<DT>(r, nch, lane);
 #pragma unroll
       for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
       const float inv = rsqrtf(ss / static_cast<float>(p.K) + p.x_eps);
@@ -754,21 +774,31 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
   for (int m = 0; m < MM; ++m)
     xr[m] = static_cast<const T*>(p.x) + (m < p.M ? m : 0) * p.ldx + 8 * hk;
 
+  // Load group at steps sb, sb + 16, ... (clamped to the last step; steps past the end
+  // count with a zero weight when consumed).
+  const int64_t s_last = nsteps - 1;
+  u32x4 wv[kGvU], nv[kGvU];
+  V8 xv[kGvU][MM];
+  auto load = [&](int64_t sb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < kGvU; ++u) {
+      const int64_t st = sb + 16 * u < nsteps ? sb + 16 * u : s_last;
+      wv[u] = wb[st * 64];
+#pragma unroll
+      for (int m = 0; m < MM; ++m) xv[u][m] = *reinterpret_cast<const V8*>(xr[m] + st * kStepK);
+      if constexpr (NORM)
+        nv[u] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.x_norm_w) + st * kStepK + 8 * hk);
+    }
+  };
+  int64_t sb = tid >> 4;
+  load(sb);  // the first group's loads are in flight while the norm below runs
+
   if constexpr (NORM) {  // inverse RMS of each row, add_rmsnorm_vec_kernel's order
     if (wave == 0) {
       const int nch = static_cast<int>(p.K >> 3);
       for (int64_t m = 0; m < p.M; ++m) {
         const T* const r = static_cast<const T*>(p.x) + m * p.ldx;
-        float ss = 0.0f;
-        for (int i = 0; 64 * i < nch; ++i) {
-          const bool ok = lane + 64 * i < nch;
-          const V8 v = *reinterpret_cast<const V8*>(r + 8 * (ok ? lane + 64 * i : 0));
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const float x = ok ? Ty<DT>::f(v[k]) : 0.0f;
-            ss = __builtin_fmaf(x, x, ss);
-          }
-        }
+        float ss = row_sumsq<DT>(r, nch, lane);
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
         if (lane == 0) s_inv[m] = rsqrtf(ss / static_cast<float>(p.K) + p.x_eps);
@@ -783,25 +813,13 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
   float acc[MM];
 #pragma unroll
   for (int m = 0; m < MM; ++m) acc[m] = 0.0f;
-  const int64_t s_last = nsteps - 1;
-  for (int64_t s0 = tid >> 4; s0 < nsteps; s0 += 16 * kGvU) {
-    u32x4 wv[kGvU], nv[kGvU];
-    V8 xv[kGvU][MM];
-#pragma unroll
-    for (int u = 0; u < kGvU; ++u) {
-      const int64_t st = s0 + 16 * u < nsteps ? s0 + 16 * u : s_last;
-      wv[u] = wb[st * 64];
-#pragma unroll
-      for (int m = 0; m < MM; ++m) xv[u][m] = *reinterpret_cast<const V8*>(xr[m] + st * kStepK);
-      if constexpr (NORM)
-        nv[u] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.x_norm_w) + st * kStepK + 8 * hk);
-    }
-    // Steps past the end were loaded (clamped) and count with a zero weight: consuming
-    // every load unconditionally keeps the compiler from sinking them behind a branch.
+  for (;;) {
+    // Consuming every loaded step (a zero weight past the end) keeps the compiler from
+    // sinking the loads behind a branch.
 #pragma unroll
     for (int u = 0; u < kGvU; ++u) {
       const u32x4 zero = {0u, 0u, 0u, 0u};
-      const V8 w8 = __builtin_bit_cast(V8, s0 + 16 * u < nsteps ? wv[u] : zero);
+      const V8 w8 = __builtin_bit_cast(V8, sb + 16 * u < nsteps ? wv[u] : zero);
 #pragma unroll
       for (int m = 0; m < MM; ++m) {
 #pragma unroll
@@ -813,6 +831,9 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
         }
       }
     }
+    sb += 16 * kGvU;
+    if (sb >= nsteps) break;
+    load(sb);
   }
   // column sums: lanes j, j+8, ..., j+56 of a wave, then the 4 waves in order
 #pragma unroll
