@@ -77,10 +77,25 @@ struct Params {
   int32_t vec_ok;
 };
 
-// Workspace: [ctl: ticket counter + error word][flags: ncb ints][carry: ncb*16*64*... floats][bc]
+// Scan modes.  kChained: a unit starts from its predecessor's carried state (waits for
+// its flag).  kSplit runs two launches over the same units: kSummary scans every segment
+// from a zero state, all at once, and records the segment's local end state and its
+// sum of delta2 per channel; kFromSummary then starts segment s from the state folded
+// out of the summaries of segments 0 .. s-1 (h = exp2(A * sum delta2) * h + h_local),
+// so no unit waits.  The split costs a second pass over the inputs; it pays when the
+// chains (batch * dim / 64) are far fewer than the workgroups the chip holds.
+enum Mode { kChained = 0, kSummary = 1, kFromSummary = 2 };
+constexpr int64_t kSplitMaxChains = 128;  // the workspace holds summaries up to this many chains
+constexpr int64_t kSplitMaxSeg = 32;      // ... of up to this many segments each
+
+// Workspace: [ctl: ticket counters + error word][flags: ncb ints][carry: ncb*G*SPL*64
+// floats][bc: packed B/C][summaries: ncb*kSplitMaxSeg*(G*SPL*64 + 64) floats, only for
+// dstate <= 16 and ncb <= kSplitMaxChains]
 struct WsLayout {
-  size_t flags, carry, bc, total;
+  size_t flags, carry, bc, sum, total;
 };
+
+inline bool split_capable(int64_t ncb, int64_t groups) { return groups == 8 && ncb <= kSplitMaxChains; }
 
 inline WsLayout ws_layout(int64_t batch, int64_t dim, int64_t groups, int64_t spl, int64_t seqlen) {
   const int64_t ncb = batch * ceil_div(dim, kCPW);
@@ -88,7 +103,11 @@ inline WsLayout ws_layout(int64_t batch, int64_t dim, int64_t groups, int64_t sp
   w.flags = 256;
   w.carry = static_cast<size_t>(round_up(w.flags + 4 * ncb, 256));
   w.bc = static_cast<size_t>(round_up(w.carry + 4 * ncb * groups * spl * kCPW, 256));
-  w.total = w.bc + static_cast<size_t>(4 * batch * groups * padded_len(seqlen) * 2 * spl);
+  w.sum = static_cast<size_t>(
+      round_up(w.bc + static_cast<size_t>(4 * batch * groups * padded_len(seqlen) * 2 * spl), 256));
+  w.total = w.sum;
+  if (split_capable(ncb, groups))
+    w.total += static_cast<size_t>(4 * ncb * kSplitMaxSeg * (groups * spl * kCPW + kCPW));
   return w;
 }
 
@@ -176,11 +195,12 @@ __device__ __forceinline__ float softplus_log2(float x) {
 }
 
 // ---------------------------------------------------------------------------
-template <int DT, int LAYOUT, int SPL, int G, bool VEC>
+template <int DT, int LAYOUT, int SPL, int G, bool VEC, int MODE>
 __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
     const Params p, const void* __restrict__ u_, const void* __restrict__ delta_,
     const void* __restrict__ z_, void* __restrict__ y_, const float* __restrict__ bc_,
-    float* __restrict__ state_out_, int* __restrict__ ctl_, float* __restrict__ carry_) {
+    float* __restrict__ state_out_, int* __restrict__ ctl_, float* __restrict__ carry_,
+    int* __restrict__ tick_, float* __restrict__ sum_) {
   using T = typename Ty<DT>::T;
   constexpr int NT = kCPW * G;
   constexpr int EPT = kCPW * kT / NT;  // elements per thread per tile
@@ -192,6 +212,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
   constexpr int BCF = G * kT * 2 * SPL;  // floats of B/C per tile
   constexpr int BCV = BCF / 4;
   constexpr int BCPT = (BCV + NT - 1) / NT;
+  constexpr int64_t SB = G * SPL * kCPW + kCPW;  // floats per segment summary
 
   // LDS tiles of delta2, delta2*u and the G partial y's.  Time-contiguous inputs stage
   // them channel-major ([channel][time], rows of kTP floats); channel-contiguous
@@ -223,7 +244,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
 
   for (;;) {
     // ---- claim a unit (segment-major tickets) ----
-    if (tid == 0) s_ticket = atomicAdd(&ctl_[0], 1);
+    if (tid == 0) s_ticket = atomicAdd(tick_, 1);
     __syncthreads();
     const int64_t unit = s_ticket;
     __syncthreads();
@@ -237,6 +258,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
 
     // ---- per-lane constants ----
     float Av[SPL], h[SPL];
+    float dsum = 0.0f;  // kSummary: sum of delta2 over the segment (this lane's channel)
     {
       const int64_t d = d0 + lane;
 #pragma unroll
@@ -296,11 +318,11 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
         if constexpr (LAYOUT == kTimeContig) {  // unit stride along time
           ru = *reinterpret_cast<const VE*>(ub + tc);
           rd = *reinterpret_cast<const VE*>(db + tc);
-          rz = *reinterpret_cast<const VE*>(zb + tc);
+          if constexpr (MODE != kSummary) rz = *reinterpret_cast<const VE*>(zb + tc);
         } else {
           ru = *reinterpret_cast<const VE*>(ub + tc * p.us2);
           rd = *reinterpret_cast<const VE*>(db + tc * p.ds2);
-          rz = *reinterpret_cast<const VE*>(zb + tc * zs2);
+          if constexpr (MODE != kSummary) rz = *reinterpret_cast<const VE*>(zb + tc * zs2);
         }
       } else {
 #pragma unroll
@@ -309,7 +331,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
           const int64_t dc = in ? d0 + ec(j) : 0, tc = in ? t0 + et(j) : 0;
           ru[j] = static_cast<const T*>(u_)[b * p.us0 + dc * p.us1 + tc * p.us2];
           rd[j] = static_cast<const T*>(delta_)[b * p.ds0 + dc * p.ds1 + tc * p.ds2];
-          rz[j] = zsrc[b * zs0 + dc * zs1 + tc * zs2];
+          if constexpr (MODE != kSummary) rz[j] = zsrc[b * zs0 + dc * zs1 + tc * zs2];
         }
       }
     };
@@ -318,7 +340,17 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
     load_raw(MM_SLOT(1), (tile0 + 1) * kT);
 
     // ---- carried state from the previous segment of this chain ----
-    if (seg > 0) {
+    if (MODE == kFromSummary && seg > 0) {
+      // fold the summaries of segments 0 .. seg-1 (written by the kSummary launch)
+      for (int64_t j = 0; j < seg; ++j) {
+        const float* sb = sum_ + (cb * p.nseg + j) * SB;
+        const float dl = sb[G * SPL * kCPW + lane];
+#pragma unroll
+        for (int k = 0; k < SPL; ++k)
+          h[k] = __builtin_fmaf(exp2_hw(Av[k] * dl), h[k], sb[(g * kCPW + lane) * SPL + k]);
+      }
+    }
+    if (MODE == kChained && seg > 0) {
       if (tid == 0) {
         int spins = 0;
         while (__hip_atomic_load(&ctl_[64 + cb], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
@@ -355,8 +387,10 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
         const float d2 = p.softplus ? softplus_log2<DT>(dr) : dr * kLog2e;
         dtv[j] = d2;
         duv[j] = d2 * uu;
-        yskip[j] = Dv[j] * uu;
-        gate[j] = has_z ? silu_f(Ty<DT>::f(rz[j])) : 1.0f;
+        if constexpr (MODE != kSummary) {
+          yskip[j] = Dv[j] * uu;
+          gate[j] = has_z ? silu_f(Ty<DT>::f(rz[j])) : 1.0f;
+        }
       }
       if (!full) {
 #pragma unroll
@@ -422,6 +456,24 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
         }
         const float dts[4] = {cur.d4.x, cur.d4.y, cur.d4.z, cur.d4.w};
         const float dus[4] = {cur.u4.x, cur.u4.y, cur.u4.z, cur.u4.w};
+        if constexpr (MODE == kSummary) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int k = 0; k < SPL; ++k) {
+              const float a = exp2_hw(dts[j] * Av[k]);
+              h[k] = __builtin_fmaf(a, h[k], dus[j] * cur.bc[j][k]);
+            }
+            dsum += dts[j];
+          }
+          // Without the y stores nothing observable follows the updates, and the compiler
+          // sinks the whole recurrence past the later barriers, keeping every tile's LDS
+          // values live (and spilling).  An opaque use per group keeps it in order.
+#pragma unroll
+          for (int k = 0; k < SPL; ++k) asm volatile("" : "+v"(h[k]));
+          asm volatile("" : "+v"(dsum));
+          continue;
+        }
         float ys[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -442,6 +494,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
         }
       }
       __syncthreads();
+      if constexpr (MODE == kSummary) return;
 
       // ---- epilogue: y = (sum_g partial + D*u) * SiLU(z) -> HBM ----
       float yv[EPT];
@@ -490,7 +543,12 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
 #undef MM_SLOT
 
     // ---- hand the state on, or write the final state ----
-    if (seg + 1 < p.nseg) {
+    if constexpr (MODE == kSummary) {
+      float* sb = sum_ + (cb * p.nseg + seg) * SB;
+#pragma unroll
+      for (int k = 0; k < SPL; ++k) sb[(g * kCPW + lane) * SPL + k] = h[k];
+      if (g == 0) sb[G * SPL * kCPW + lane] = dsum;
+    } else if (MODE == kChained && seg + 1 < p.nseg) {
       float* cp = carry_ + ((cb * G + g) * kCPW + lane) * SPL;
 #pragma unroll
       for (int k = 0; k < SPL; ++k)
@@ -504,7 +562,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
       if (tid == 0)
         __hip_atomic_store(&ctl_[64 + cb], static_cast<int>(seg + 1), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
-    } else if (state_out_ != nullptr) {
+    } else if (state_out_ != nullptr && seg + 1 == p.nseg) {
       const int64_t d = d0 + lane;
       if (d < p.dim) {
 #pragma unroll
@@ -568,9 +626,34 @@ inline void pick_segments(Params& p, int64_t grid) {
   p.nunits = p.ncb * p.nseg;
 }
 
+// Split or chained (see Mode).  In tile-times: the chained makespan is pick_segments'
+// estimate; the split one is ceil(units / grid) rounds of the summary pass (~3/4 of a
+// tile per tile: no epilogue, no z) plus as many of the main pass, each unit with one
+// tile of overhead, plus two tiles for the second launch.  Segments of the split are
+// whole groups of four tiles, at most kSplitMaxSeg per chain.
+inline bool pick_split(Params& p, int64_t grid_sum, int64_t grid_main) {
+  const int64_t ntiles = p.Lp / kT;
+  const int64_t chained4 = 4 * ceil_div(p.nunits, std::max<int64_t>(1, std::min(grid_main, p.ncb))) *
+                           (p.seg_tiles + 1);
+  int64_t best = INT64_MAX, best_st = 0;
+  for (int64_t n = 2; n <= kSplitMaxSeg; ++n) {
+    const int64_t st = round_up(ceil_div(ntiles, n), kTGroup);
+    const int64_t ns = ceil_div(ntiles, st);
+    if (ns < 2) continue;
+    const int64_t units = p.ncb * ns;
+    const int64_t c4 = ceil_div(units, grid_sum) * (3 * st + 4) + ceil_div(units, grid_main) * 4 * (st + 1) + 8;
+    if (c4 < best) best = c4, best_st = st;
+  }
+  if (best_st == 0 || best >= chained4) return false;
+  p.seg_tiles = best_st;
+  p.nseg = ceil_div(ntiles, best_st);
+  p.nunits = p.ncb * p.nseg;
+  return true;
+}
+
 template <int DT, int LAYOUT, int SPL, int G, bool VEC>
 void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w) {
-  auto kern = scan_kernel<DT, LAYOUT, SPL, G, VEC>;
+  auto kern = scan_kernel<DT, LAYOUT, SPL, G, VEC, kChained>;
   char* ws = static_cast<char*>(a->workspace);
   int* ctl = reinterpret_cast<int*>(ws);
   float* carry = reinterpret_cast<float*>(ws + w.carry);
@@ -579,9 +662,30 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
   if (per_cu == 0) per_cu = resident_per_cu(kern, kCPW * G);
   const int64_t resident = static_cast<int64_t>(num_cus()) * per_cu;
   pick_segments(p, resident);
+  if constexpr (G == 8) {
+    if (split_capable(p.ncb, G) && a->workspace_bytes >= w.total) {
+      auto ksum = scan_kernel<DT, LAYOUT, SPL, G, VEC, kSummary>;
+      auto kmain = scan_kernel<DT, LAYOUT, SPL, G, VEC, kFromSummary>;
+      static int per_cu_sum = 0, per_cu_main = 0;
+      if (per_cu_sum == 0) per_cu_sum = resident_per_cu(ksum, kCPW * G);
+      if (per_cu_main == 0) per_cu_main = resident_per_cu(kmain, kCPW * G);
+      const int64_t rs = static_cast<int64_t>(num_cus()) * per_cu_sum;
+      const int64_t rm = static_cast<int64_t>(num_cus()) * per_cu_main;
+      if (pick_split(p, rs, rm)) {
+        float* sum = reinterpret_cast<float*>(ws + w.sum);
+        hipLaunchKernelGGL(ksum, dim3(static_cast<unsigned>(std::min(p.nunits, rs))), dim3(kCPW * G),
+                           0, s, p, a->u, a->delta, a->z, a->y, bc, a->state_out, ctl, carry,
+                           ctl, sum);
+        hipLaunchKernelGGL(kmain, dim3(static_cast<unsigned>(std::min(p.nunits, rm))), dim3(kCPW * G),
+                           0, s, p, a->u, a->delta, a->z, a->y, bc, a->state_out, ctl, carry,
+                           ctl + 2, sum);
+        return;
+      }
+    }
+  }
   const int64_t grid = std::min<int64_t>(p.nunits, resident);
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(kCPW * G), 0, s, p, a->u,
-                     a->delta, a->z, a->y, bc, a->state_out, ctl, carry);
+                     a->delta, a->z, a->y, bc, a->state_out, ctl, carry, ctl, nullptr);
 }
 
 template <int DT, int LAYOUT, int SPL, int G>
