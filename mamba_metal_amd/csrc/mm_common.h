@@ -88,6 +88,35 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float log2_hw(float x) { return __builtin_amdgcn_logf(x); }
+
+// 2^x to ~1 ulp without a one-sided bias: 2^n * 2^r with n = rint(x) and r = x - n in
+// [-1/2, 1/2] (exact), 2^r from its Taylor series sum_k (r ln 2)^k / k! to k = 7 (the
+// dropped terms are < 1e-8 relative), Horner with fma.  A decay exp2(delta2 * A) enters
+// the state once per step, so over a state's memory (thousands of steps when |A| delta is
+// ~1e-3) a per-step error that always leans one way adds up linearly; v_exp_f32's does
+// and moves long fp32 scans by ~1e-5 relative, this one's rounding errors do not.
+__device__ __forceinline__ float exp2_acc(float x) {
+  x = fminf(fmaxf(x, -160.0f), 128.0f);  // past either end the result is 0 or +inf anyway
+  const float n = __builtin_rintf(x);
+  const float r = x - n;
+  float q = 1.5252733804059840e-05f;      // (ln 2)^7 / 7!
+  q = __builtin_fmaf(q, r, 1.5403530393381606e-04f);  // (ln 2)^6 / 6!
+  q = __builtin_fmaf(q, r, 1.3333558146428443e-03f);  // (ln 2)^5 / 5!
+  q = __builtin_fmaf(q, r, 9.6181291076284772e-03f);  // (ln 2)^4 / 4!
+  q = __builtin_fmaf(q, r, 5.5504108664821580e-02f);  // (ln 2)^3 / 3!
+  q = __builtin_fmaf(q, r, 2.4022650695910071e-01f);  // (ln 2)^2 / 2!
+  q = __builtin_fmaf(q, r, 6.9314718055994531e-01f);  // ln 2
+  q = __builtin_fmaf(q, r, 1.0f);
+  return __builtin_ldexpf(q, static_cast<int>(n));
+}
+
+// The scan's decay: fp32 inputs take exp2_acc (parity at rtol 1e-5 over long
+// sequences); fp16 / bf16 inputs (tolerance 1e-3) take v_exp_f32.
+template <int DT>
+__device__ __forceinline__ float exp2_decay(float x) {
+  if constexpr (DT == MM_F32) return exp2_acc(x);
+  else return exp2_hw(x);
+}
 __device__ __forceinline__ float rcp_hw(float x) { return __builtin_amdgcn_rcpf(x); }
 
 // RMSNorm output element: round(x * inv * w) to DT with the fp32 product rounded first.

@@ -347,7 +347,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
         const float dl = sb[G * SPL * kCPW + lane];
 #pragma unroll
         for (int k = 0; k < SPL; ++k)
-          h[k] = __builtin_fmaf(exp2_hw(Av[k] * dl), h[k], sb[(g * kCPW + lane) * SPL + k]);
+          h[k] = __builtin_fmaf(exp2_decay<DT>(Av[k] * dl), h[k], sb[(g * kCPW + lane) * SPL + k]);
       }
     }
     if (MODE == kChained && seg > 0) {
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
           for (int j = 0; j < 4; ++j) {
 #pragma unroll
             for (int k = 0; k < SPL; ++k) {
-              const float a = exp2_hw(dts[j] * Av[k]);
+              const float a = exp2_decay<DT>(dts[j] * Av[k]);
               h[k] = __builtin_fmaf(a, h[k], dus[j] * cur.bc[j][k]);
             }
             dsum += dts[j];
@@ -480,7 +480,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
           float acc = 0.0f;
 #pragma unroll
           for (int k = 0; k < SPL; ++k) {
-            const float a = exp2_hw(dts[j] * Av[k]);
+            const float a = exp2_decay<DT>(dts[j] * Av[k]);
             h[k] = __builtin_fmaf(a, h[k], dus[j] * cur.bc[j][k]);
             acc = __builtin_fmaf(h[k], cur.bc[j][SPL + k], acc);
           }
