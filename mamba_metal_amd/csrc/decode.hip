@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kBlock) void ssm_step_kernel(const Params p) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int n = n4 + k;
-        const float a = exp2_hw(dtl * as[k]);
+        const float a = exp2_decay<DT>(dtl * as[k]);
         hs[k] = __builtin_fmaf(a, hs[k], du * ld<DT>(p.B, b * p.Bsb + n));
         acc = __builtin_fmaf(hs[k], ld<DT>(p.C, b * p.Csb + n), acc);
       }
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(kBlock) void ssm_step_kernel(const Params p) {
 #pragma unroll
     for (int n = 0; n < NS; ++n) {
       if (n < N) {
-        const float a = exp2_hw(dtl * Ap[n]);
+        const float a = exp2_decay<DT>(dtl * Ap[n]);
         const float hn = __builtin_fmaf(a, hp[n], du * ld<DT>(p.B, b * p.Bsb + n));
         hp[n] = hn;
         acc = __builtin_fmaf(hn, ld<DT>(p.C, b * p.Csb + n), acc);
@@ -331,7 +331,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_dtproj_kernel(const
     float acc = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float a = exp2_hw(dtv * Al[k]);
+      const float a = exp2_decay<DT>(dtv * Al[k]);
       hs[k] = __builtin_fmaf(a, hs[k], du * s_B[bb][q * 4 + k]);
       acc = __builtin_fmaf(hs[k], s_C[bb][q * 4 + k], acc);
     }
@@ -470,7 +470,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_mfma_kernel(const F
     float yacc = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float a = exp2_hw(dtv * Al[k]);
+      const float a = exp2_decay<DT>(dtv * Al[k]);
       hs[k] = __builtin_fmaf(a, hs[k], du * s_B[bb][q * 4 + k]);
       yacc = __builtin_fmaf(hs[k], s_C[bb][q * 4 + k], yacc);
     }
