@@ -270,6 +270,23 @@ int mm_pack_linear_weight(const void* w, void* packed, int64_t N, int64_t K, int
 size_t mm_decode_linear_workspace_size(int64_t M, int64_t N, int64_t K);
 int mm_decode_linear(const mm_linear_params* params, void* stream);
 
+/* in_proj + conv-window step + x_proj of one decode step -- replaces the
+ * in_proj -> conv window -> x_proj chain of MambaBlock.step (mamba_block.py:166-182):
+ * runs mm_decode_linear(params) (epilogue MM_LIN_CONV), then
+ * xp_y[m, n] = round(sum_k conv_out[m, k] * W_x[n, k]) for n < xp_n, k < n_conv, with
+ * xp_w_packed the mm_pack_linear_weight copy of the (xp_n, n_conv) x_proj weight and
+ * xp_y rows of stride ld_xp in params->dtype.  Where the in_proj shape allows (4-wave
+ * K-resident workgroups, no input RMSNorm, workgroup columns on one side of n_conv,
+ * xp_n <= 256 and a multiple of 4) the x_proj products are taken in in_proj's conv
+ * epilogue from the conv outputs still on chip, as fp32 partials per workgroup,
+ * summed in a fixed order by one small kernel; otherwise the two GEMMs run one after
+ * the other.  The workspace (params->workspace) must hold
+ * mm_decode_in_proj_xproj_workspace_size bytes, 16-byte aligned. */
+size_t mm_decode_in_proj_xproj_workspace_size(int64_t M, int64_t N, int64_t K, int64_t n_conv,
+                                              int64_t xp_n);
+int mm_decode_in_proj_xproj(const mm_linear_params* params, const void* xp_w_packed,
+                            int64_t xp_n, void* xp_y, int64_t ld_xp, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Greedy token choice -- replaces `mx.argmax(logits[:, -1, :], axis=-1)` of
  * generate_fast (generate.py:91-93): out[r] = index of the largest x[r, 0:n]

@@ -94,6 +94,13 @@ struct LinParams {
   void* norm_out;
   float* partials;  // split calls: [ks][M][N] fp32
   const void* x_norm_w;  // input RMSNorm weight (K,), or null
+  // x_proj folded into in_proj's conv epilogue (mm_decode_in_proj_xproj): packed
+  // x_proj weight (xp_n rows, K = n_conv, xp_nsteps 16-k steps), fp32 partial planes
+  // [n_conv / TN][M][xp_n] and the (M, xp_n) output.
+  const u32x4* xp_w;
+  float* xp_part;
+  void* xp_y;
+  int64_t xp_n, xp_nsteps, ld_xp;
   int64_t M, N, K, ldx, ldy, ldr, ldc, ldn, n_conv;
   float eps, x_eps;
   int32_t ks;       // K splits across workgroups (grid.y)
@@ -211,11 +218,12 @@ __device__ __forceinline__ float row_sumsq(const typename Ty<DT>::T* r, int nch,
 // 8*(i/4) + 4*(l/32) + i%4, column l%32.
 __device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
-template <int DT, int KSW, int MT, int NT, int EPI, bool NORM = false>
+template <int DT, int KSW, int MT, int NT, int EPI, bool NORM = false, bool XP = false>
 __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
   using T = typename Ty<DT>::T;
   using V8 = typename Ty<DT>::V8;
   static_assert(!NORM || MT == 1, "the input RMSNorm covers rows 0..7 of one m-tile");
+  static_assert(!XP || (EPI == MM_LIN_CONV && KSW == 4 && !NORM), "x_proj rides the 4-wave conv epilogue");
   constexpr int XI = MT * 4;                 // X load instructions per chunk (8 rows each)
   constexpr int NACC = MT * NT * 16;         // accumulator floats per lane
   constexpr int kWaveLds = kXLds > NACC * 64 * 4 ? kXLds : NACC * 64 * 4;
@@ -386,6 +394,23 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
         }
     return;
   } else {
+    // XP: this wave's x_proj weight tiles (32 rows each, waves w and w + 4), loaded
+    // here so that their latency overlaps the partial-tile exchange and the conv step.
+    constexpr int XPT = 2;                 // x_proj column tiles per wave (xp_n <= 256)
+    constexpr int XST = TN / kStepK;       // x_proj k steps of this workgroup (its TN columns)
+    u32x4 wx[XP ? XPT : 1][XP ? XST : 1];
+    const bool xp_here = XP && n0 < p.n_conv;  // workgroup-uniform (n_conv % TN == 0)
+    if constexpr (XP) {
+      const int64_t ntx = (p.xp_n + kTileN - 1) / kTileN;
+      const int64_t s0 = n0 / kStepK;
+#pragma unroll
+      for (int i = 0; i < XPT; ++i) {
+        const int64_t j = wave + 4 * i;
+        const int64_t jj = j < ntx && xp_here ? j : 0;
+#pragma unroll
+        for (int g = 0; g < XST; ++g) wx[i][g] = p.xp_w[(jj * p.xp_nsteps + (xp_here ? s0 : 0) + g) * 64 + lane];
+      }
+    }
     // Partial tiles -> this wave's LDS slot (register-major, lane-contiguous).
     float* const part = reinterpret_cast<float*>(xs);
 #pragma unroll
@@ -432,6 +457,9 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
           rb[ms[u] * p.ldr + ns[u]] = Ty<DT>::from(Ty<DT>::f(old[u]) + Ty<DT>::f(Ty<DT>::from(vals[u])));
     } else {
       T4* const sb = static_cast<T4*>(p.conv_state);
+      T cov[XP ? EPT : 1];  // XP: this thread's conv outputs, the x_proj operand
+#pragma unroll
+      for (int u = 0; u < (XP ? EPT : 1); ++u) cov[u] = Ty<DT>::from(0.0f);
 #pragma unroll
       for (int u = 0; u < EPT; ++u) {
         const int64_t m = ms[u], n = ns[u];
@@ -449,12 +477,95 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
           nw[2] = win[u][3];
           nw[3] = xr;
           sb[m * p.n_conv + n] = nw;
-          st<DT>(p.conv_out, m * p.ldc + n, silu_f(a));
+          const T co = Ty<DT>::from(silu_f(a));
+          static_cast<T*>(p.conv_out)[m * p.ldc + n] = co;
+          if constexpr (XP) cov[u] = co;
         } else {
           st<DT>(p.y, m * p.ldy + (n - p.n_conv), vals[u]);
         }
       }
+      if constexpr (XP) {
+        if (xp_here) {
+          // x_proj partial of this workgroup's K range (its TN conv columns):
+          // part[t][m][n] = sum_k conv_out[m, n0 + k] * W_x[n, n0 + k].  The conv
+          // outputs go to LDS (slot 0, the X-chunk layout) as the MFMA A operand.
+          __syncthreads();  // every wave has read the partial-sum slots
+          T* const xt = reinterpret_cast<T*>(smem);
+#pragma unroll
+          for (int u = 0; u < EPT; ++u) xt[(e_row0 + u * kRowStep) * (kRowBytes / 2) + e_col] = cov[u];
+          __syncthreads();
+          const int64_t ntx = (p.xp_n + kTileN - 1) / kTileN;
+          f32x16 xacc[MT][XPT];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < XPT; ++i)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) xacc[mt][i][r] = 0.0f;
+#pragma unroll
+          for (int g = 0; g < XST; ++g)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const u32x4 a = *reinterpret_cast<const u32x4*>(smem + mt * 32 * kRowBytes + rd_off + g * 32);
+#pragma unroll
+              for (int i = 0; i < XPT; ++i)
+                if (wave + 4 * i < ntx) xacc[mt][i] = mfma<DT>(a, wx[i][g], xacc[mt][i]);
+            }
+          float* const dst = p.xp_part + t * p.M * p.xp_n;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < XPT; ++i)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int64_t m = 32 * mt + acc_row(r, lane);
+                const int64_t n = 32 * (wave + 4 * i) + (lane & 31);
+                if (m < p.M && n < p.xp_n) dst[m * p.xp_n + n] = xacc[mt][i][r];
+              }
+        }
+      }
     }
+  }
+}
+
+// x_proj planes of mm_decode_in_proj_xproj summed: y[m, n] = round(sum_p part[p][m][n]).
+// A workgroup covers 16 four-column groups; its 16 thread slices each sum a contiguous
+// run of planes in order (all loads of a run issued together), then slice 0 adds the 16
+// run sums in order -- a fixed summation order, so results are reproducible.
+template <int DT>
+__global__ __launch_bounds__(256) void xp_reduce_kernel(const LinParams p, int64_t nplanes) {
+  __shared__ f32x4 s_sum[16][16];
+  constexpr int kRun = 8;  // planes per thread slice and pass (loads in flight)
+  const int gq = threadIdx.x & 15, sl = threadIdx.x >> 4;
+  const int64_t nq = (p.xp_n + 3) / 4;
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * 16 + gq;
+  const int64_t qc = q < p.M * nq ? q : 0;
+  const int64_t m = qc / nq, n = (qc % nq) * 4;
+  const int64_t plane = p.M * p.xp_n;
+  const int64_t per = (nplanes + 15) / 16;
+  const int64_t p0 = sl * per;
+  const int64_t p1 = p0 + per < nplanes ? p0 + per : nplanes;
+  f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int64_t pb = p0; pb < p1; pb += kRun) {
+    f32x4 a[kRun];
+#pragma unroll
+    for (int k = 0; k < kRun; ++k) {
+      const int64_t pp = pb + k < p1 ? pb + k : p0;
+      a[k] = *reinterpret_cast<const f32x4*>(p.xp_part + pp * plane + m * p.xp_n + n);
+    }
+#pragma unroll
+    for (int k = 0; k < kRun; ++k)
+      if (pb + k < p1) v += a[k];
+  }
+  s_sum[sl][gq] = v;
+  __syncthreads();
+  if (sl == 0 && q < p.M * nq) {
+    f32x4 tot = s_sum[0][gq];
+#pragma unroll
+    for (int k = 1; k < 16; ++k) tot += s_sum[k][gq];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (n + u < p.xp_n) st<DT>(p.xp_y, m * p.ld_xp + n + u, tot[u]);
   }
 }
 
@@ -957,6 +1068,49 @@ void launch_main(const LinParams& p, int32_t epi, const Plan& pl, dim3 grid, hip
   else launch_ksw<DT, 1, 1>(p, epi, pl.ksw, grid, s);
 }
 
+// in_proj + conv window + x_proj partials (then xp_reduce_kernel): the 4-wave linear_kernel
+// shapes only (see xp_fusable).
+template <int DT>
+void launch_main_xp(const LinParams& p, const Plan& pl, dim3 grid, hipStream_t s) {
+  const dim3 block(4 * 64);
+  if (p.M > 32 && pl.nt == 2)
+    hipLaunchKernelGGL((linear_kernel<DT, 4, 2, 2, MM_LIN_CONV, false, true>), grid, block, 0, s, p);
+  else if (p.M > 32)
+    hipLaunchKernelGGL((linear_kernel<DT, 4, 2, 1, MM_LIN_CONV, false, true>), grid, block, 0, s, p);
+  else if (pl.nt == 2)
+    hipLaunchKernelGGL((linear_kernel<DT, 4, 1, 2, MM_LIN_CONV, false, true>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((linear_kernel<DT, 4, 1, 1, MM_LIN_CONV, false, true>), grid, block, 0, s, p);
+  const int64_t nplanes = p.n_conv / (kTileN * pl.nt);
+  const dim3 rgrid(static_cast<unsigned>(ceil_div(p.M * ceil_div(p.xp_n, 4), 16)));
+  hipLaunchKernelGGL((xp_reduce_kernel<DT>), rgrid, dim3(256), 0, s, p, nplanes);
+}
+
+// Whether mm_decode_in_proj_xproj folds x_proj into in_proj's conv epilogue: the call
+// must run linear_kernel with K in the workgroup over 4 waves (no GEMV, no shared-X
+// kernel, no K split, no input RMSNorm), every workgroup's columns must lie on one side
+// of n_conv, and x_proj must have at most 8 column tiles, a multiple of 4 columns.
+inline bool xp_fusable(int64_t M, int64_t N, int64_t K, int64_t n_conv, int64_t xp_n, bool x_norm) {
+  if (x_norm || M < 1 || M > kMaxM || N < 1 || K % kChunkK != 0 || use_gemv(M, N)) return false;
+  const Plan pl = plan(N, K);
+  if (pl.nw > 0 || pl.ks != 1 || pl.ksw != 4) return false;
+  const int64_t tn = kTileN * pl.nt;
+  return xp_n >= 4 && xp_n <= 8 * kTileN && xp_n % 4 == 0 && n_conv >= tn && n_conv % tn == 0 &&
+         n_conv % kChunkK == 0;
+}
+
+inline size_t xp_workspace(int64_t M, int64_t N, int64_t K, int64_t n_conv, int64_t xp_n) {
+  const Plan pl = plan(N, K);
+  return static_cast<size_t>(n_conv / (kTileN * pl.nt)) * static_cast<size_t>(M * xp_n) * 4;
+}
+
+struct XpArgs {
+  const void* w;
+  int64_t n;
+  void* y;
+  int64_t ld;
+};
+
 template <int DT, int NW, int MT>
 void launch_share_epi(const LinParams& p, int32_t epi, dim3 grid, hipStream_t s) {
   const dim3 block(NW * 64);
@@ -1084,10 +1238,14 @@ size_t mm_decode_linear_workspace_size(int64_t M, int64_t N, int64_t K) {
   return static_cast<size_t>(pl.ks * M * N * 4);
 }
 
-int mm_decode_linear(const mm_linear_params* prm, void* stream) {
-  using namespace mm;
-  using namespace mm::gemm;
-  clear_error();
+}  // extern "C"
+
+namespace mm {
+namespace gemm {
+
+// mm_decode_linear; with xp (only when xp_fusable) in_proj's conv epilogue also runs
+// x_proj on the conv outputs.
+static int decode_linear_core(const mm_linear_params* prm, void* stream, const XpArgs* xp) {
   if (!prm) return fail(MM_ERR_NULL_POINTER, "params is NULL");
   const mm_linear_params& q = *prm;
   if (!q.x || !q.w_packed) return fail(MM_ERR_NULL_POINTER, "x and w_packed are required");
@@ -1130,7 +1288,8 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
   }
   if (q.M == 0 || q.N == 0) return MM_OK;
   const Plan pl = plan(q.N, q.K);
-  const size_t need = mm_decode_linear_workspace_size(q.M, q.N, q.K);
+  const size_t need = xp ? xp_workspace(q.M, q.N, q.K, q.n_conv, xp->n)
+                         : mm_decode_linear_workspace_size(q.M, q.N, q.K);
   if (need > 0) {
     if (!q.workspace || q.workspace_bytes < need)
       return fail(MM_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need,
@@ -1162,6 +1321,12 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
   p.ldc = q.ldc;
   p.n_conv = q.n_conv;
   p.ks = use_gemv(q.M, q.N) ? 1 : pl.ks;  // the GEMV keeps K in the workgroup
+  p.xp_w = xp ? static_cast<const u32x4*>(xp->w) : nullptr;
+  p.xp_part = xp ? static_cast<float*>(q.workspace) : nullptr;
+  p.xp_y = xp ? xp->y : nullptr;
+  p.xp_n = xp ? xp->n : 0;
+  p.xp_nsteps = xp ? q.n_conv / kStepK : 0;
+  p.ld_xp = xp ? xp->ld : 0;
   const dim3 grid(static_cast<unsigned>(ceil_div(q.N, kTileN * (pl.nw > 0 ? pl.nw : pl.nt))),
                   static_cast<unsigned>(pl.ks));
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1169,6 +1334,11 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
   const bool fused_norm = norm && fused_norm_ok(p, q.dtype, q.resid, q.norm_w, q.norm_out);
   const int32_t epi = norm ? MM_LIN_RESID : q.epilogue;  // RESID_NORM = RESID + norm pass
   const int32_t main_epi = pl.ks > 1 ? kPartial : epi;
+  if (xp) {
+    if (q.dtype == MM_F16) launch_main_xp<MM_F16>(p, pl, grid, s);
+    else launch_main_xp<MM_BF16>(p, pl, grid, s);
+    return check_launch("decode_in_proj_xproj");
+  }
   if (use_gemv(q.M, q.N)) {
     if (q.dtype == MM_F16) launch_gemv<MM_F16>(p, epi, s);
     else launch_gemv<MM_BF16>(p, epi, s);
@@ -1198,6 +1368,65 @@ int mm_decode_linear(const mm_linear_params* prm, void* stream) {
                           q.dtype, q.dtype, stream);
   }
   return check_launch("decode_linear");
+}
+
+}  // namespace gemm
+}  // namespace mm
+
+extern "C" {
+
+int mm_decode_linear(const mm_linear_params* prm, void* stream) {
+  mm::clear_error();
+  return mm::gemm::decode_linear_core(prm, stream, nullptr);
+}
+
+size_t mm_decode_in_proj_xproj_workspace_size(int64_t M, int64_t N, int64_t K, int64_t n_conv,
+                                              int64_t xp_n) {
+  using namespace mm::gemm;
+  if (M <= 0 || N <= 0 || K <= 0 || n_conv <= 0 || xp_n <= 0) return 0;
+  // enough for either path: an input RMSNorm (not known here) turns the fusion off
+  const size_t two = std::max(mm_decode_linear_workspace_size(M, N, K),
+                              mm_decode_linear_workspace_size(M, xp_n, n_conv));
+  if (xp_fusable(M, N, K, n_conv, xp_n, false))
+    return std::max(xp_workspace(M, N, K, n_conv, xp_n), two);
+  return two;
+}
+
+int mm_decode_in_proj_xproj(const mm_linear_params* prm, const void* xp_w_packed, int64_t xp_n,
+                            void* xp_y, int64_t ld_xp, void* stream) {
+  using namespace mm;
+  using namespace mm::gemm;
+  clear_error();
+  if (!prm) return fail(MM_ERR_NULL_POINTER, "params is NULL");
+  if (prm->epilogue != MM_LIN_CONV) return fail(MM_ERR_SHAPE, "in_proj needs the MM_LIN_CONV epilogue");
+  if (!xp_w_packed || !xp_y) return fail(MM_ERR_NULL_POINTER, "xp_w_packed and xp_y are required");
+  if (xp_n < 1 || xp_n > 0x7fffffffLL) return fail(MM_ERR_SHAPE, "xp_n=%lld out of range", (long long)xp_n);
+  if (ld_xp < xp_n) return fail(MM_ERR_LAYOUT, "ld_xp < xp_n");
+  if (!aligned(xp_w_packed, 16)) return fail(MM_ERR_LAYOUT, "xp_w_packed must be 16-byte aligned");
+  if (prm->n_conv % kChunkK != 0 || prm->ldc % 8 != 0 || !aligned(prm->conv_out, 16))
+    return fail(MM_ERR_LAYOUT, "x_proj's K (n_conv) must be a multiple of %d and conv_out rows "
+                "16-byte aligned", kChunkK);
+  const mm_linear_params& q = *prm;
+  if (xp_fusable(q.M, q.N, q.K, q.n_conv, xp_n, q.x_norm_w != nullptr)) {
+    const XpArgs xa{xp_w_packed, xp_n, xp_y, ld_xp};
+    return decode_linear_core(prm, stream, &xa);
+  }
+  int st = decode_linear_core(prm, stream, nullptr);
+  if (st != MM_OK) return st;
+  mm_linear_params x = {};
+  x.x = q.conv_out;
+  x.w_packed = xp_w_packed;
+  x.y = xp_y;
+  x.M = q.M;
+  x.N = xp_n;
+  x.K = q.n_conv;
+  x.ldx = q.ldc;
+  x.ldy = ld_xp;
+  x.dtype = q.dtype;
+  x.epilogue = MM_LIN_STORE;
+  x.workspace = q.workspace;
+  x.workspace_bytes = q.workspace_bytes;
+  return decode_linear_core(&x, stream, nullptr);
 }
 
 }  // extern "C"

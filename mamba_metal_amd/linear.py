@@ -190,6 +190,46 @@ def decode_linear_resid_norm_(resid: torch.Tensor, x: torch.Tensor, w: torch.Ten
     return out
 
 
+def xproj_weight_ok(x: torch.Tensor, w_x: torch.Tensor, n_conv: int) -> bool:
+    """Whether w_x can be decode_in_proj_conv_xproj's x_proj weight for conv width n_conv."""
+    return (w_x.dim() == 2 and w_x.shape[1] == n_conv and w_x.dtype == x.dtype and w_x.is_cuda
+            and _rows_ok(w_x) and n_conv % K_MULTIPLE == 0)
+
+
+def decode_in_proj_conv_xproj(x, w, conv_state, conv_w, conv_b, w_x, x_norm=None):
+    """decode_in_proj_conv followed by x_proj: returns (x_conv (M, n_conv), z (M, n_z),
+    x_dbl (M, N_x) = x_conv @ w_x.T) through mm_decode_in_proj_xproj, which takes the
+    x_proj products inside in_proj's conv epilogue where the shape allows."""
+    dev = _lib.require_cuda(x, w, conv_state, conv_w, conv_b, w_x)
+    if not in_proj_conv_ok(x, w, conv_state, conv_w, conv_b):
+        raise ValueError("decode_in_proj_conv_xproj: unsupported layout (see in_proj_conv_ok)")
+    M, N = x.shape[0], w.shape[0]
+    n_conv = conv_state.shape[1]
+    if not xproj_weight_ok(x, w_x, n_conv):
+        raise ValueError("w_x must be (N_x, n_conv) in x's dtype with 16-byte aligned rows and "
+                         f"n_conv % {K_MULTIPLE} == 0")
+    prm = _base(x, w, LIN_CONV, x_norm)
+    x_conv = torch.empty((M, n_conv), dtype=x.dtype, device=dev)
+    z = torch.empty((M, N - n_conv), dtype=x.dtype, device=dev)
+    x_dbl = torch.empty((M, w_x.shape[0]), dtype=x.dtype, device=dev)
+    prm.y, prm.ldy = z.data_ptr(), z.stride(0)
+    prm.conv_state, prm.conv_w = conv_state.data_ptr(), conv_w.data_ptr()
+    prm.conv_b = _lib.ptr(conv_b)
+    prm.conv_out, prm.ldc = x_conv.data_ptr(), x_conv.stride(0)
+    prm.n_conv = n_conv
+    lib = _lib.load()
+    ws = _workspace(dev, lib.mm_decode_in_proj_xproj_workspace_size(M, N, prm.K, n_conv,
+                                                                     w_x.shape[0]))
+    if ws is not None:
+        prm.workspace, prm.workspace_bytes = ws.data_ptr(), ws.numel()
+    with torch.cuda.device(dev):
+        st = lib.mm_decode_in_proj_xproj(ctypes.byref(prm), packed_weight(w_x).data_ptr(),
+                                         w_x.shape[0], x_dbl.data_ptr(), x_dbl.stride(0),
+                                         _lib.stream_of(dev))
+    _lib.check(st, "mm_decode_in_proj_xproj")
+    return x_conv, z, x_dbl
+
+
 def in_proj_conv_ok(x, w, conv_state, conv_w, conv_b) -> bool:
     n_conv = conv_state.shape[1] if conv_state.dim() == 3 else -1
     return (decode_linear_ok(x, w) and conv_state.dim() == 3 and conv_state.shape[2] == 4

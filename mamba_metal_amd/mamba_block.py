@@ -31,10 +31,10 @@ import torch.nn.functional as F
 
 from mamba_metal_amd.conv1d import causal_conv1d, conv_step
 from mamba_metal_amd.decode import ssm_step_dtproj
-from mamba_metal_amd.linear import (NORM_IN_MAX_M, decode_in_proj_conv, decode_linear,
-                                    decode_linear_ok, decode_linear_resid_,
+from mamba_metal_amd.linear import (NORM_IN_MAX_M, decode_in_proj_conv, decode_in_proj_conv_xproj,
+                                    decode_linear, decode_linear_ok, decode_linear_resid_,
                                     decode_linear_resid_norm_, in_proj_conv_ok, norm_in_ok,
-                                    split_k)
+                                    split_k, xproj_weight_ok)
 from mamba_metal_amd.norm import add_rmsnorm
 from mamba_metal_amd.selective_scan import selective_scan_into
 
@@ -166,16 +166,23 @@ class MambaBlock(nn.Module):
                 fold = (x_norm.weight, x_norm.eps)
             else:
                 x = add_rmsnorm(x, None, x_norm.weight, x_norm.eps)
-        if conv_ok:
-            x_conv, z = decode_in_proj_conv(x, W_in, conv_state, self.conv1d.weight,
-                                            self.conv1d.bias, x_norm=fold)
-        else:
-            xz = self.in_proj(x)                               # (B, 2*d_inner)
-            x_main, z = xz[:, :di], xz[:, di:]
-            x_conv = conv_step(conv_state, x_main, self.conv1d.weight, self.conv1d.bias,
-                               apply_silu=True)                # (B, d_inner)
         W_x = self.x_proj.weight
-        x_dbl = decode_linear(x_conv, W_x) if decode_linear_ok(x_conv, W_x) else self.x_proj(x_conv)
+        if conv_ok and xproj_weight_ok(x, W_x, di):
+            # in_proj + conv window + x_proj in one call (x_proj inside in_proj's epilogue
+            # where the shape allows)
+            x_conv, z, x_dbl = decode_in_proj_conv_xproj(x, W_in, conv_state, self.conv1d.weight,
+                                                         self.conv1d.bias, W_x, x_norm=fold)
+        else:
+            if conv_ok:
+                x_conv, z = decode_in_proj_conv(x, W_in, conv_state, self.conv1d.weight,
+                                                self.conv1d.bias, x_norm=fold)
+            else:
+                xz = self.in_proj(x)                           # (B, 2*d_inner)
+                x_main, z = xz[:, :di], xz[:, di:]
+                x_conv = conv_step(conv_state, x_main, self.conv1d.weight, self.conv1d.bias,
+                                   apply_silu=True)            # (B, d_inner)
+            x_dbl = (decode_linear(x_conv, W_x) if decode_linear_ok(x_conv, W_x)
+                     else self.x_proj(x_conv))
         dt_pre, Bm, Cm = self._split_xdbl(x_dbl)
         y = ssm_step_dtproj(ssm_state, x_conv, dt_pre, self.dt_proj.weight, self._A(), Bm, Cm,
                             dt_bias=self.dt_proj.bias, D=self.D, z=z)

@@ -176,6 +176,47 @@ def test_decode_in_proj_conv(dev, K, di, M, dtype):
     assert_close(st.float().cpu().numpy(), ref_st, tol, tol * 4, "conv state")
 
 
+# in_proj + conv window + x_proj (mm_decode_in_proj_xproj).  Fused -- x_proj products
+# taken in in_proj's conv epilogue, fp32 partial planes summed by one kernel: 2.8B shape
+# (two 32-column tiles per wave, 80 planes of 64 conv columns), 130M at batch 16 (one
+# m-tile) and 33 (two), an x_proj of 256 columns (every wave two tiles).  Falling back to
+# two GEMMs: batch 3 (GEMV in_proj), an x_proj width that is not a multiple of 4, the
+# input RMSNorm.  The in_proj outputs must equal decode_in_proj_conv's bit for bit; x_dbl
+# is checked against the fp32 product of the returned conv outputs.
+@pytest.mark.parametrize("M,K,di,nx,norm,fused", [
+    (64, 2560, 5120, 192, False, True), (16, 768, 1536, 80, False, True),
+    (33, 768, 1536, 80, False, True), (64, 512, 640, 256, False, True),
+    (3, 768, 1536, 80, False, False), (8, 768, 1536, 50, False, False),
+    (8, 768, 1536, 80, True, False)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_in_proj_conv_xproj(dev, M, K, di, nx, norm, fused, dtype):
+    from mamba_metal_amd import _lib
+    from mamba_metal_amd.linear import decode_in_proj_conv, decode_in_proj_conv_xproj
+
+    g = torch.Generator(device=dev).manual_seed(7 + M + di + nx)
+    x = torch.randn((M, K), generator=g, device=dev).to(dtype)
+    w = (torch.randn((2 * di, K), generator=g, device=dev) * 0.05).to(dtype)
+    cw = torch.randn((di, 1, 4), generator=g, device=dev).to(dtype)
+    cb = torch.randn((di,), generator=g, device=dev).to(dtype)
+    wx = (torch.randn((nx, di), generator=g, device=dev) * 0.05).to(dtype)
+    st_a = torch.randn((M, di, 4), generator=g, device=dev).to(dtype)
+    st_b = st_a.clone()
+    st_c = st_a.clone()
+    fold = (torch.rand((K,), generator=g, device=dev).to(dtype) + 0.5, 1e-5) if norm else None
+    x_conv, z = decode_in_proj_conv(x, w, st_a, cw, cb, x_norm=fold)
+    x_conv2, z2, x_dbl = decode_in_proj_conv_xproj(x, w, st_b, cw, cb, wx, x_norm=fold)
+    torch.cuda.synchronize()
+    assert torch.equal(x_conv2, x_conv) and torch.equal(z2, z) and torch.equal(st_b, st_a)
+    _check(x_dbl, _ref(x_conv, wx), dtype, "x_proj")
+    _, _, x_dbl2 = decode_in_proj_conv_xproj(x, w, st_c, cw, cb, wx, x_norm=fold)
+    assert torch.equal(x_dbl2, x_dbl)                      # fixed summation order
+    # the fused shapes size the workspace for (n_conv / tile width) fp32 planes of M x nx
+    if fused:
+        tn = 64 if 2 * di >= 256 * 32 else 32
+        ws = _lib.load().mm_decode_in_proj_xproj_workspace_size(M, 2 * di, K, di, nx)
+        assert ws >= (di // tn) * M * nx * 4
+
+
 # Input RMSNorm folded into the operand load: the product must be bit-identical to the
 # separate add_rmsnorm + GEMM (the kernel recomputes the norm in add_rmsnorm's order).
 # Shapes: 130M in_proj (conv) at M = 1, 3, 8; 2.8B in_proj (two tiles per wave); a
