@@ -12,6 +12,8 @@ Shape violations raise AssertionError with the reference's conditions
 (selective_scan.py:46-50).  Arithmetic is fp32 inside the HIP kernel for every
 dtype (the reference's generated MSL promotes half loads to float).  Inputs may
 be any strided view -- no contiguous copies are made; the kernel reads strides.
+y has u's layout when u is a channel-contiguous view (e.g. a transposed (batch, seqlen,
+dim) tensor), otherwise the (batch, dim, seqlen) row-major layout.
 Mixed dtypes are promoted exactly (to float32) and y is rounded back to u.dtype,
 which is what the reference's float arithmetic + half store does.
 """
@@ -151,7 +153,14 @@ def selective_scan(
     dd = delta if delta.dtype == xdt else delta.to(xdt)
     zz = z if (z is None or z.dtype == xdt) else z.to(xdt)
 
-    y = torch.empty((batch, dim, seqlen), dtype=xdt, device=u.device)
+    # y takes u's layout when u is a channel-contiguous view (a transposed (batch, seqlen,
+    # dim) tensor, as the model passes): with every operand along channels the kernel runs
+    # its channel-contiguous fast path instead of the strided one a (batch, dim, seqlen)
+    # y would force (B=64, D=5120, L=512 fp16: 1.26 -> ~1.0 ms).
+    if uu.stride(1) == 1 and uu.stride(2) != 1:
+        y = torch.empty_like(uu, dtype=xdt)
+    else:
+        y = torch.empty((batch, dim, seqlen), dtype=xdt, device=u.device)
     state = torch.empty((batch, dim, dstate), dtype=torch.float32, device=u.device) \
         if return_state else None
     selective_scan_into(uu, dd, A, B, C, y, D=D, z=zz, delta_softplus=delta_softplus,

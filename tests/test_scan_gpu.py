@@ -172,6 +172,24 @@ def test_layouts(oracle_lib, dev, layout, dtype):
     check(oracle_lib, dev, inp, f"layout {layout}", dtype=dtype, softplus=True, layout=layout)
 
 
+def test_channel_contiguous_views_keep_their_layout(oracle_lib, dev):
+    """Transposed (batch, seqlen, dim) views in: y comes back in the same layout (so the
+    kernel's channel-contiguous path runs end to end) with the oracle's values."""
+    from mamba_metal_amd import selective_scan
+
+    inp = fp16_inputs(2, 128, 16, 512, seed=8)
+    t = lambda a: torch.as_tensor(a).to(dev, torch.float16).transpose(1, 2).contiguous().transpose(1, 2)
+    u, d, z, B, C = (t(inp[k]) for k in ("u", "delta", "z", "B", "C"))
+    A = torch.as_tensor(inp["A"]).to(dev)
+    D = torch.as_tensor(inp["D"]).to(dev)
+    y, h = selective_scan(u, d, A, B, C, D=D, z=z, delta_softplus=True, return_state=True)
+    torch.cuda.synchronize()
+    assert y.shape == u.shape and y.stride() == u.stride()
+    yo, ho = oracle_scan(oracle_lib, inp, torch.float16, softplus=True)
+    assert_close(y.float().cpu().numpy(), yo, 1e-3, 1e-3, "channel-contiguous y")
+    assert_close(h.cpu().numpy(), ho, 1e-3, 1e-3, "channel-contiguous state")
+
+
 def test_unaligned_seqlen_uses_gather_path(oracle_lib, dev):
     # L % 8 != 0 disables the 16-byte vector path for the (batch, dim, seqlen) layout.
     check(oracle_lib, dev, fp16_inputs(2, 40, 16, 101, seed=6), "L=101 fp16", dtype=torch.float16,
