@@ -217,6 +217,40 @@ def test_decode_linear_validation(lib):
     assert lib.mm_pack_linear_weight(FAKE, FAKE, 50, 64, 64, _lib.F32, None) == _lib.ERR_DTYPE
 
 
+def test_decode_in_proj_xproj_validation(lib):
+    """mm_decode_in_proj_xproj: the in_proj params as for mm_decode_linear (conv
+    epilogue required) plus the x_proj weight / output, all checked before any launch."""
+    def call(xp_w=FAKE, xp_n=192, xp_y=FAKE, ld_xp=192, **kw):
+        prm = _lib.LinearParams()
+        prm.x = prm.w_packed = prm.y = prm.conv_state = prm.conv_w = prm.conv_out = FAKE
+        prm.M, prm.N, prm.K = 64, 10240, 2560
+        prm.ldx, prm.ldy, prm.ldc = 2560, 5120, 5120
+        prm.n_conv = 5120
+        prm.dtype, prm.epilogue = _lib.F16, 2   # MM_LIN_CONV
+        for k, v in kw.items():
+            setattr(prm, k, v)
+        return lib.mm_decode_in_proj_xproj(ctypes.byref(prm), xp_w, xp_n, xp_y, ld_xp, None)
+    assert lib.mm_decode_in_proj_xproj(None, FAKE, 192, FAKE, 192, None) == _lib.ERR_NULL_POINTER
+    assert call(epilogue=0) == _lib.ERR_SHAPE                 # in_proj must carry the conv step
+    assert call(xp_w=None) == _lib.ERR_NULL_POINTER
+    assert call(xp_y=None) == _lib.ERR_NULL_POINTER
+    assert call(xp_n=0) == _lib.ERR_SHAPE
+    assert call(ld_xp=100) == _lib.ERR_LAYOUT
+    assert call(xp_w=FAKE + 8) == _lib.ERR_LAYOUT
+    assert call(n_conv=5100, ldc=5100) == _lib.ERR_LAYOUT    # x_proj's K must be a multiple of 64
+    assert call(conv_out=FAKE + 8) == _lib.ERR_LAYOUT
+    # the fused path needs its partial planes (80 x 64 x 192 fp32 here)
+    need = lib.mm_decode_in_proj_xproj_workspace_size(64, 10240, 2560, 5120, 192)
+    assert need >= 80 * 64 * 192 * 4
+    assert call() == _lib.ERR_WORKSPACE
+    assert call(workspace=FAKE, workspace_bytes=need - 1) == _lib.ERR_WORKSPACE
+    assert call(M=0) == _lib.OK
+    # batch <= 4 runs in_proj as a GEMV and x_proj as its own (split-K) GEMM
+    assert lib.mm_decode_in_proj_xproj_workspace_size(2, 10240, 2560, 5120, 192) == \
+        lib.mm_decode_linear_workspace_size(2, 192, 5120)
+    assert lib.mm_decode_in_proj_xproj_workspace_size(0, 10240, 2560, 5120, 192) == 0
+
+
 def test_argmax_validation(lib):
     out = FAKE
     assert lib.mm_argmax_rows(None, 2, 8, 8, _lib.F16, out, None) == _lib.ERR_NULL_POINTER
