@@ -246,8 +246,9 @@ def main():
     if args.only_scan:
         args.no_extra = args.no_decode = args.no_cpu = True
     if args.gpus != 1:
-        print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); the scan shards over "
-              "(batch, channel) with no exchange -- see DESIGN.md", file=sys.stderr)
+        print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); the scan would shard "
+              "over (batch, channel) with no exchange between GPUs, so one GPU's share is the "
+              "measured unit", file=sys.stderr)
         sys.exit(2)
 
     import torch
