@@ -194,6 +194,27 @@ def test_graph_decoder_matches_eager(dev, small):
     assert np.array_equal(generate_fast_ids(model, ids, 12, use_graph=True).cpu().numpy(), eager)
 
 
+@pytest.mark.parametrize("batch", [2, 12])
+def test_graph_decoder_fused_paths_match_eager(dev, batch):
+    """130m width (3 layers), fp16: the captured decode step with the batch-dependent fused
+    paths -- batch 2: GEMVs with the input norm folded into in_proj; batch 12: in_proj +
+    conv + x_proj in one call with its plane reduce -- replayed 10 times with eager work
+    between replays, token for token equal to eager steps."""
+    from mamba_metal_amd import GraphDecoder, generate_fast_ids
+
+    model, cfg = make_model(dev, dtype=torch.float16, seed=31, d_model=768, n_layer=3,
+                            vocab_size=2048, dt_rank=48)
+    ids = torch.as_tensor(np.random.default_rng(31 + batch).integers(0, cfg.vocab_size, (batch, 20)),
+                          device=dev)
+    eager = generate_fast_ids(model, ids, 10).cpu().numpy()
+    dec = GraphDecoder(model, batch, use_graph=True)
+    toks = [dec.start(ids).cpu().numpy()]
+    for _ in range(9):
+        toks.append(dec.step().cpu().numpy())
+        _ = torch.randn(1000, device=dev).sum().item()   # eager work + sync between replays
+    assert np.array_equal(np.stack(toks, 1), eager)
+
+
 def test_config1_shape_fp16_greedy_parity(dev):
     """130m shape (config 1), fp16 weights/activations, fp32 scan state: 96-token prompt,
     12 teacher-forced decode steps against the float64 oracle."""
