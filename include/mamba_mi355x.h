@@ -20,9 +20,11 @@
  *   - Return MM_OK (0) on success.  Invalid arguments are rejected by host-only
  *     validation BEFORE any HIP call, with a negative mm_status; the message is in
  *     mm_last_error() (thread-local).  A failed launch returns MM_ERR_HIP.
- *   - No global mutable state besides the thread-local error string: thread-safe.
- *     Calls on one stream are ordered; calls on different streams that share
- *     output buffers race, as any two kernels would.
+ *   - Host state: the thread-local error string, and per-device caches of launch
+ *     constants (CU count, resident workgroups per CU) that are computed once and
+ *     published with atomic stores.  Thread-safe.  Calls on one stream are ordered;
+ *     calls on different streams that share output buffers race, as any two kernels
+ *     would.
  */
 #ifndef MAMBA_MI355X_H
 #define MAMBA_MI355X_H
@@ -34,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 2
+#define MM_ABI_VERSION 3
 /* Largest d_state accepted: mamba_metal/selective_scan.py:9 (MAX_DSTATE = 64). */
 #define MM_MAX_DSTATE 64
 
@@ -124,7 +126,16 @@ typedef struct mm_scan_params {
   int32_t bc_dtype;         /* mm_dtype of B, C                                  */
   int32_t delta_softplus;   /* nonzero: apply softplus to delta                  */
   int32_t reserved;         /* must be 0                                         */
+  int32_t* status;          /* optional device int32 (NULL = none): the kernel ORs
+                               MM_SCAN_STATUS_* bits into it when y is not valid.
+                               The library never clears it, so one word can collect
+                               the outcome of many calls (e.g. every layer of a
+                               prefill); the caller zeroes it and reads it after
+                               the stream has finished. */
 } mm_scan_params;
+
+/* Bits of mm_scan_params.status (and of the workspace status word). */
+#define MM_SCAN_STATUS_HANDOFF_TIMEOUT 1 /* a segment gave up waiting for the carried state */
 
 int mm_selective_scan_fwd_strided(const mm_scan_params* p, void* stream);
 

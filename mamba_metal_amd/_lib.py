@@ -19,7 +19,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library; see module d
 
 LIB_NAME = "libmamba_mi355x.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 2
+ABI_VERSION = 3
 MAX_DSTATE = 64
 
 # mm_dtype
@@ -56,7 +56,11 @@ class ScanParams(ctypes.Structure):
         ("y_stride", _i64a3), ("B_stride", _i64a3), ("C_stride", _i64a3),
         ("A_stride", _i64a2), ("D_stride", _i64),
         ("x_dtype", _i32), ("bc_dtype", _i32), ("delta_softplus", _i32), ("reserved", _i32),
+        ("status", _vp),
     ]
+
+
+SCAN_STATUS_HANDOFF_TIMEOUT = 1
 
 
 class LinearParams(ctypes.Structure):

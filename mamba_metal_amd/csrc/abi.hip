@@ -23,6 +23,20 @@ int fail(int status, const char* fmt, ...) {
 
 void clear_error() { g_last_error[0] = '\0'; }
 
+int num_cus() {
+  static DeviceCache cache;
+  return device_cached(
+      cache,
+      [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+          n = 0;
+        return n;
+      },
+      256);
+}
+
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MM_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));

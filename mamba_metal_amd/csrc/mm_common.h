@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstddef>
 #include <cstdint>
@@ -28,6 +29,28 @@ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 inline bool aligned(const void* p, int64_t bytes) {
   return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
 }
+
+// Per-device cache of a launch constant (CU count, resident workgroups per CU of one
+// kernel).  The value is computed on first use on each device and published with an
+// atomic store; racing threads compute and store the same value, so no lock is needed.
+constexpr int kMaxDevices = 64;
+struct DeviceCache {
+  std::atomic<int> v[kMaxDevices];
+};
+template <typename F>
+int device_cached(DeviceCache& c, F compute, int fallback) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return compute();
+  int x = c.v[dev].load(std::memory_order_relaxed);
+  if (x == 0) {
+    x = compute();
+    if (x < 1) x = fallback;
+    c.v[dev].store(x, std::memory_order_relaxed);
+  }
+  return x;
+}
+// Compute units of the current device.
+int num_cus();
 
 // ---------------------------------------------------------------------------
 // Device-side element types.  All arithmetic is fp32; T is the storage type.

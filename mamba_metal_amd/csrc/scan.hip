@@ -75,6 +75,7 @@ struct Params {
   int64_t As0, As1, Ds;
   int32_t softplus;
   int32_t vec_ok;
+  int* status;  // optional persistent status word (MM_SCAN_STATUS_* bits are ORed in)
 };
 
 // Scan modes.  kChained: a unit starts from its predecessor's carried state (waits for
@@ -357,7 +358,11 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
                static_cast<int>(seg)) {
           __builtin_amdgcn_s_sleep(1);
           if (++spins > kSpinLimit) {  // never expected; keeps every wave's exit bounded
-            __hip_atomic_store(&ctl_[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&ctl_[1], MM_SCAN_STATUS_HANDOFF_TIMEOUT, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            if (p.status != nullptr)
+              __hip_atomic_fetch_or(p.status, MM_SCAN_STATUS_HANDOFF_TIMEOUT, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
             break;
           }
         }
@@ -577,26 +582,19 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Workgroups per CU each instantiation can keep resident, per device (cached).
+// Workgroups per CU an instantiation can keep resident on the current device; the
+// caller keeps one DeviceCache per instantiation.
 template <typename K>
-int resident_per_cu(K kernel, int threads) {
-  int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n < 1)
-    n = 1;
-  return n;
-}
-
-int num_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
+int resident_per_cu(DeviceCache& cache, K kernel, int threads) {
+  return device_cached(
+      cache,
+      [&] {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess)
+          n = 0;
+        return n;
+      },
+      1);
 }
 
 // Segments per chain.  A chain's segments run one after another (each waits for the
@@ -658,19 +656,19 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
   int* ctl = reinterpret_cast<int*>(ws);
   float* carry = reinterpret_cast<float*>(ws + w.carry);
   const float* bc = reinterpret_cast<const float*>(ws + w.bc);
-  static int per_cu = 0;
-  if (per_cu == 0) per_cu = resident_per_cu(kern, kCPW * G);
-  const int64_t resident = static_cast<int64_t>(num_cus()) * per_cu;
+  static DeviceCache per_cu_cache;
+  const int64_t resident =
+      static_cast<int64_t>(num_cus()) * resident_per_cu(per_cu_cache, kern, kCPW * G);
   pick_segments(p, resident);
   if constexpr (G == 8) {
     if (split_capable(p.ncb, G) && a->workspace_bytes >= w.total) {
       auto ksum = scan_kernel<DT, LAYOUT, SPL, G, VEC, kSummary>;
       auto kmain = scan_kernel<DT, LAYOUT, SPL, G, VEC, kFromSummary>;
-      static int per_cu_sum = 0, per_cu_main = 0;
-      if (per_cu_sum == 0) per_cu_sum = resident_per_cu(ksum, kCPW * G);
-      if (per_cu_main == 0) per_cu_main = resident_per_cu(kmain, kCPW * G);
-      const int64_t rs = static_cast<int64_t>(num_cus()) * per_cu_sum;
-      const int64_t rm = static_cast<int64_t>(num_cus()) * per_cu_main;
+      static DeviceCache sum_cache, main_cache;
+      const int64_t rs =
+          static_cast<int64_t>(num_cus()) * resident_per_cu(sum_cache, ksum, kCPW * G);
+      const int64_t rm =
+          static_cast<int64_t>(num_cus()) * resident_per_cu(main_cache, kmain, kCPW * G);
       if (pick_split(p, rs, rm)) {
         float* sum = reinterpret_cast<float*>(ws + w.sum);
         hipLaunchKernelGGL(ksum, dim3(static_cast<unsigned>(std::min(p.nunits, rs))), dim3(kCPW * G),
@@ -846,6 +844,7 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
   p.Ds = a->D_stride;
   p.softplus = a->delta_softplus ? 1 : 0;
   p.vec_ok = vec_ok;
+  p.status = a->status;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t nctl = 64 + p.ncb;

@@ -94,7 +94,8 @@ def generate_fast(model, tokenizer, prompt: str, max_new_tokens: int = 50,
         if on_token is not None:
             prev_text = _stream(tokenizer, prompt, generated_ids, prev_text, on_token)
         ids = torch.tensor([[next_id_int]], dtype=torch.long, device=device)
-        step_logits, conv_states, ssm_states = model.step(ids, conv_states, ssm_states)
+        step_logits, conv_states, ssm_states = model.step(ids, conv_states, ssm_states,
+                                                          inplace=True)
         next_logits = step_logits[:, 0, :]
     return prompt + tokenizer.decode(generated_ids, skip_special_tokens=True)
 
@@ -120,7 +121,7 @@ class GraphDecoder:
         self.ssms = None
 
     def _eager_step(self):
-        logits, _, _ = self.model.step(self.ids.view(-1, 1), self.convs, self.ssms)
+        logits, _, _ = self.model.step(self.ids.view(-1, 1), self.convs, self.ssms, inplace=True)
         return _argmax(logits[:, 0, :])
 
     @torch.inference_mode()
@@ -179,6 +180,8 @@ def generate_fast_ids(model, input_ids: torch.Tensor, max_new_tokens: int,
     EOS as the reference does and returns the ids before it.  use_graph replays
     a captured HIP graph per step (greedy, no EOS)."""
     B = input_ids.shape[0]
+    if max_new_tokens <= 0:
+        return torch.empty((B, 0), dtype=torch.long, device=input_ids.device)
     if use_graph and temperature == 0.0 and eos_token_id is None:
         dec = GraphDecoder(model, B, use_graph=True)
         toks = [dec.start(input_ids).clone()]
@@ -195,7 +198,7 @@ def generate_fast_ids(model, input_ids: torch.Tensor, max_new_tokens: int,
         out.append(tok)
         if i + 1 == max_new_tokens:
             break
-        step_logits, convs, ssms = model.step(tok.view(-1, 1), convs, ssms)
+        step_logits, convs, ssms = model.step(tok.view(-1, 1), convs, ssms, inplace=True)
         nxt = step_logits[:, 0, :]
     if not out:
         return torch.empty((B, 0), dtype=torch.long, device=input_ids.device)

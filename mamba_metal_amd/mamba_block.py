@@ -125,12 +125,12 @@ class MambaBlock(nn.Module):
         return y, conv_state, ssm_state
 
     def step(self, x_token: torch.Tensor, conv_state: torch.Tensor, ssm_state: torch.Tensor,
-             inplace: bool = True):
+             inplace: bool = False):
         """O(1) per-token forward (mamba_block.py:155-198).
 
-        x_token (B, 1, d_model).  The resident states are updated IN PLACE by the
-        decode kernels and returned (the reference returns fresh arrays); pass
-        inplace=False to leave the given states untouched."""
+        x_token (B, 1, d_model).  Functional by default, as the reference (which returns
+        fresh arrays): the given states are left untouched and new ones returned.  With
+        inplace=True the decode kernels update the given states in place and return them."""
         if not inplace:
             conv_state = conv_state.clone()
             ssm_state = ssm_state.clone()

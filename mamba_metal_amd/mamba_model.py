@@ -48,7 +48,9 @@ class MambaResidualBlock(nn.Module):
         y, conv_state, ssm_state = self.mixer.prefill(self.norm(x))
         return x + y, conv_state, ssm_state
 
-    def step(self, x_token, conv_state, ssm_state, inplace: bool = True):
+    def step(self, x_token, conv_state, ssm_state, inplace: bool = False):
+        """Functional by default, as the reference's step: the given states are left
+        untouched and fresh ones returned; ``inplace=True`` updates them in place."""
         y, new_conv, new_ssm = self.mixer.step(self.norm(x_token), conv_state, ssm_state,
                                                inplace=inplace)
         return x_token + y, new_conv, new_ssm
@@ -129,10 +131,13 @@ class MambaModel(nn.Module):
             h = h[:, -1:, :]
         return self._head(h), convs, ssms
 
-    def step(self, input_ids: torch.Tensor, conv_states, ssm_states, inplace: bool = True):
+    def step(self, input_ids: torch.Tensor, conv_states, ssm_states, inplace: bool = False):
         """One new token per sequence (B, 1) -> (logits (B, 1, vocab), states).
 
-        States are updated in place and returned (see MambaBlock.step)."""
+        Functional by default, as the reference's step (mamba_model.py:112-127): the
+        given state lists are left untouched and new state tensors are returned.  With
+        ``inplace=True`` the decode kernels update the given tensors in place (no copy;
+        what generate_fast and GraphDecoder use) and the same tensors are returned."""
         if not inplace:
             conv_states = [t.clone() for t in conv_states]
             ssm_states = [t.clone() for t in ssm_states]

@@ -40,19 +40,44 @@ def _common_dtype(*ts):
     return torch.float32
 
 
-_LAST_WS: dict = {}   # device -> workspace of the last call (holds its status word)
+_STATUS: dict = {}   # device -> persistent int32 status word every scan ORs into
+
+
+def _dev_of(device) -> torch.device:
+    if device is None:
+        return torch.device("cuda", torch.cuda.current_device())
+    dev = torch.device(device)
+    return dev if dev.index is not None else torch.device("cuda", torch.cuda.current_device())
+
+
+def _status_word(dev: torch.device) -> torch.Tensor:
+    w = _STATUS.get(dev)
+    if w is None:
+        w = torch.zeros(1, dtype=torch.int32, device=dev)
+        _STATUS[dev] = w
+    return w
 
 
 def scan_status(device=None) -> int:
-    """Status word of the last scan on ``device`` (synchronises that device): 0 when
-    every time segment received its predecessor's carried state; nonzero when a bounded
-    hand-off wait gave up (not expected to happen), i.e. that call's y is not valid."""
-    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    ws = _LAST_WS.get(dev)
-    if ws is None:
+    """OR of the status bits of every scan on ``device`` since the last
+    ``reset_scan_status`` (synchronises that device).  0 when every time segment of
+    every call received its predecessor's carried state; nonzero
+    (``_lib.SCAN_STATUS_HANDOFF_TIMEOUT``) when a bounded hand-off wait gave up -- not
+    expected to happen -- and some call's y is not valid."""
+    dev = _dev_of(device)
+    w = _STATUS.get(dev)
+    if w is None:
         return 0
     torch.cuda.synchronize(dev)
-    return int(ws[4:8].view(torch.int32).item())
+    return int(w.item())
+
+
+def reset_scan_status(device=None) -> None:
+    """Clear the status word of ``device`` (ordered on its current stream)."""
+    dev = _dev_of(device)
+    w = _STATUS.get(dev)
+    if w is not None:
+        w.zero_()
 
 
 def selective_scan_into(u, delta, A, B, C, y, *, D=None, z=None, delta_softplus=False,
@@ -82,7 +107,6 @@ def selective_scan_into(u, delta, A, B, C, y, *, D=None, z=None, delta_softplus=
 
     ws_bytes = lib.mm_selective_scan_workspace_size(batch, dim, dstate, seqlen)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
-    _LAST_WS[dev] = ws
 
     p = _lib.ScanParams()
     p.u, p.delta, p.A, p.B, p.C = u.data_ptr(), delta.data_ptr(), A.data_ptr(), B.data_ptr(), C.data_ptr()
@@ -105,6 +129,7 @@ def selective_scan_into(u, delta, A, B, C, y, *, D=None, z=None, delta_softplus=
     p.bc_dtype = _lib.dtype_code(bcdt)
     p.delta_softplus = 1 if delta_softplus else 0
     p.reserved = 0
+    p.status = _status_word(dev).data_ptr()
     with torch.cuda.device(dev):
         st = lib.mm_selective_scan_fwd_strided(p, _lib.stream_of(dev))
     _lib.check(st, "mm_selective_scan_fwd_strided")

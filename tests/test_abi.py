@@ -48,7 +48,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_version_and_status_names(lib):
-    assert lib.mm_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.mm_abi_version() == _lib.ABI_VERSION == 3
     assert lib.mm_status_name(0) == b"MM_OK"
     assert lib.mm_status_name(-3) == b"MM_ERR_DSTATE"
     assert lib.mm_status_name(-99) == b"MM_ERR_UNKNOWN"
