@@ -53,7 +53,10 @@ def _dev_of(device) -> torch.device:
 def _status_word(dev: torch.device) -> torch.Tensor:
     w = _STATUS.get(dev)
     if w is None:
-        w = torch.zeros(1, dtype=torch.int32, device=dev)
+        # a normal tensor even when the first scan runs under inference_mode, so that
+        # reset_scan_status() may clear it anywhere
+        with torch.inference_mode(False):
+            w = torch.zeros(1, dtype=torch.int32, device=dev)
         _STATUS[dev] = w
     return w
 

@@ -83,3 +83,31 @@ def assert_close(actual, expected, rtol, atol, what=""):
         raise AssertionError(
             f"{what}: {int(bad.sum())}/{bad.size} elements outside rtol={rtol} atol={atol}; "
             f"worst at {i}: got {actual[i]!r} expected {expected[i]!r} (max abs err {err.max():.3e})")
+
+
+def check_greedy(got, gpu_logits, ref_logits, n, what, max_exempt_frac=0.25, tol=2e-2):
+    """Teacher-forced logits within fp16 tolerance, and the GPU's greedy id equal to the
+    oracle's argmax at every step where the oracle's top-2 margin exceeds twice the
+    measured logit error of this run (there no error of that size can flip the argmax;
+    below it a flip is possible and the step is counted as exempt, not hidden)."""
+    errs = [float(np.abs(gpu_logits[s].cpu().numpy() - ref_logits[s].numpy()).max()) for s in range(n)]
+    err = max(errs)
+    exempt = []
+    for s in range(n):
+        g, r = gpu_logits[s].cpu().numpy(), ref_logits[s].numpy()
+        assert_close(g, r, tol, tol, f"{what}: step {s} logits")
+        for row in range(r.shape[0]):
+            top2 = np.sort(r[row])[-2:]
+            margin = float(top2[1] - top2[0])
+            if margin > 2 * err:
+                assert got[row, s] == int(np.argmax(r[row])), \
+                    f"{what}: step {s} row {row}: margin {margin:.4f} > 2 x err {err:.2e}"
+            else:
+                exempt.append((s, row, margin))
+    total = n * ref_logits[0].shape[0]
+    scale = max(float(np.abs(ref_logits[s].numpy()).max()) for s in range(n))
+    print(f"[greedy] {what}: per-step max logit error {[f'{e:.1e}' for e in errs]}, "
+          f"max |logit| {scale:.2f}")
+    print(f"[greedy] {what}: max logit error {err:.2e}; {len(exempt)} of {total} argmax checks "
+          f"exempt (oracle top-2 margin <= {2 * err:.2e}): {exempt}")
+    assert len(exempt) <= max_exempt_frac * total
