@@ -139,6 +139,23 @@ typedef struct mm_scan_params {
 
 int mm_selective_scan_fwd_strided(const mm_scan_params* p, void* stream);
 
+/* Allocation-free form of mm_selective_scan_fwd.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, semantics and
+ * results as mm_selective_scan_fwd, without the workspace: the library keeps one scan
+ * workspace of MM_SCAN_SCRATCH_BYTES per device in a static device array, held until
+ * the process ends.  Shapes whose mm_selective_scan_workspace_size exceeds
+ * MM_SCAN_SCRATCH_BYTES are rejected with MM_ERR_WORKSPACE (host-side, before any HIP
+ * call).  It calls no allocating routine.  Every call on a device uses that device's
+ * array, so calls that overlap in time on one device race (order them on one stream);
+ * the array's status word is not visible to the caller. */
+#define MM_SCAN_SCRATCH_BYTES (32u << 20)
+int mm_selective_scan_fwd_noalloc(const void* u, const void* delta, const float* A,
+                                  const void* B, const void* C, const float* D, const void* z,
+                                  void* y, float* ssm_state_out, int64_t batch, int64_t dim,
+                                  int64_t dstate, int64_t seqlen, int32_t x_dtype,
+                                  int32_t bc_dtype, int32_t delta_softplus, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* (b) Causal depthwise conv1d over time, channels-last -- replaces
  *     nn.Conv1d(groups=d_inner, padding=d_conv-1)[:, :L] + nn.silu of

@@ -61,6 +61,7 @@ class ScanParams(ctypes.Structure):
 
 
 SCAN_STATUS_HANDOFF_TIMEOUT = 1
+SCAN_SCRATCH_BYTES = 32 << 20   # MM_SCAN_SCRATCH_BYTES
 
 
 class LinearParams(ctypes.Structure):
@@ -85,6 +86,8 @@ _SIGNATURES = {
     "mm_selective_scan_fwd": (
         [_vp] * 9 + [_i64] * 4 + [_i32, _i32, _i32, _vp, _sz, _vp], ctypes.c_int),
     "mm_selective_scan_fwd_strided": ([ctypes.POINTER(ScanParams), _vp], ctypes.c_int),
+    "mm_selective_scan_fwd_noalloc": ([_vp] * 9 + [_i64] * 4 + [_i32, _i32, _i32, _vp],
+                                      ctypes.c_int),
     "mm_causal_conv1d_fwd": (
         [_vp] * 5 + [_i64] * 4 + [_i64a3, _i64a3, _i64a2, _i32, _i32, _i32, _vp], ctypes.c_int),
     "mm_decode_conv_step": (

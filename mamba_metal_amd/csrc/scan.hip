@@ -901,3 +901,86 @@ int mm_selective_scan_fwd(const void* u, const void* delta, const float* A, cons
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free entry point.  Its workspace is `scratch`, a file-scope device array:
+// every GPU the library runs on holds its own copy (MM_SCAN_SCRATCH_BYTES) until the
+// process ends.  In host code the array's name is only a stand-in for the symbol, so
+// its device address is taken once per device with hipGetSymbolAddress and kept in
+// scratch_ptr[device]; kernels are only ever given that address.  The launches are
+// those of mm_selective_scan_fwd (the B/C pack kernel clears the work-queue counter
+// and flags at the start of every call, so the previous call's contents do not
+// matter).  Calls that overlap in time on one GPU share the array and race.
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[MM_SCAN_SCRATCH_BYTES];
+
+std::atomic<void*> scratch_ptr[mm::kMaxDevices];
+
+// Device address of this device's `scratch` (looked up on the first call on a device).
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return mm::fail(MM_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= mm::kMaxDevices)
+    return mm::fail(MM_ERR_HIP, "device %d outside the library's %d-device table", dev,
+                    mm::kMaxDevices);
+  void* p = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return mm::fail(MM_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                      hipGetErrorString(e));
+    scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return MM_OK;
+}
+
+}  // namespace
+
+extern "C" int mm_selective_scan_fwd_noalloc(const void* u, const void* delta, const float* A,
+                                             const void* B, const void* C, const float* D,
+                                             const void* z, void* y, float* ssm_state_out,
+                                             int64_t batch, int64_t dim, int64_t dstate,
+                                             int64_t seqlen, int32_t x_dtype, int32_t bc_dtype,
+                                             int32_t delta_softplus, void* stream) {
+  using namespace mm;
+  clear_error();
+  mm_scan_params a = {};
+  a.u = u;
+  a.delta = delta;
+  a.A = A;
+  a.B = B;
+  a.C = C;
+  a.D = D;
+  a.z = z;
+  a.y = y;
+  a.state_out = ssm_state_out;
+  a.batch = batch;
+  a.dim = dim;
+  a.dstate = dstate;
+  a.seqlen = seqlen;
+  a.x_dtype = x_dtype;
+  a.bc_dtype = bc_dtype;
+  a.delta_softplus = delta_softplus;
+  // host-only checks first (no HIP call before the arguments are known to be valid)
+  int st = scan::validate(&a);
+  if (st != MM_OK) return st;
+  if (batch == 0 || dim == 0) return MM_OK;
+  const size_t need = mm_selective_scan_workspace_size(batch, dim, dstate, seqlen);
+  if (need > MM_SCAN_SCRATCH_BYTES)
+    return fail(MM_ERR_WORKSPACE,
+                "batch=%lld dim=%lld dstate=%lld seqlen=%lld needs %zu bytes of scan workspace; "
+                "the allocation-free entry point holds %zu (use mm_selective_scan_fwd with a "
+                "caller-allocated workspace)",
+                (long long)batch, (long long)dim, (long long)dstate, (long long)seqlen, need,
+                static_cast<size_t>(MM_SCAN_SCRATCH_BYTES));
+  void* ptr = nullptr;
+  st = scratch_address(&ptr);
+  if (st != MM_OK) return st;
+  return mm_selective_scan_fwd(u, delta, A, B, C, D, z, y, ssm_state_out, batch, dim, dstate,
+                               seqlen, x_dtype, bc_dtype, delta_softplus, ptr,
+                               MM_SCAN_SCRATCH_BYTES, stream);
+}

@@ -269,3 +269,20 @@ def test_zero_sizes_are_noops(lib):
     assert lib.mm_causal_conv1d_fwd(FAKE, FAKE, None, FAKE, None, 1, 0, 8, 4, s3, s3, s2, 1, 1, 1,
                                     None) == _lib.OK
     assert lib.mm_pair_scan(FAKE, FAKE, None, FAKE, 0, None) == _lib.OK
+
+
+def test_noalloc_scan_rejects_oversize_host_side(lib):
+    # a shape whose workspace exceeds the static per-device array is refused before any
+    # HIP call; invalid arguments are refused as by mm_selective_scan_fwd
+    batch, dim, seqlen = 8, 5120, 65536
+    assert lib.mm_selective_scan_workspace_size(batch, dim, 16, seqlen) > _lib.SCAN_SCRATCH_BYTES
+    st = lib.mm_selective_scan_fwd_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, None,
+                                           batch, dim, 16, seqlen, _lib.F16, _lib.F16, 1, None)
+    assert st == _lib.ERR_WORKSPACE
+    assert b"allocation-free" in lib.mm_last_error()
+    assert lib.mm_selective_scan_fwd_noalloc(None, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, None,
+                                             1, 64, 16, 64, 1, 1, 1, None) == _lib.ERR_NULL_POINTER
+    assert lib.mm_selective_scan_fwd_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, None,
+                                             1, 64, 65, 64, 1, 1, 1, None) == _lib.ERR_DSTATE
+    assert lib.mm_selective_scan_fwd_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, None,
+                                             0, 64, 16, 64, 1, 1, 1, None) == _lib.OK
