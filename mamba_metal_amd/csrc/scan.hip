@@ -224,8 +224,19 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
   constexpr int TILE_F = (LAYOUT == kTimeContig) ? kCPW * kTP : kT * kCP;
   __shared__ __attribute__((aligned(16))) float s_dt[TILE_F];
   __shared__ __attribute__((aligned(16))) float s_du[TILE_F];
-  __shared__ __attribute__((aligned(16))) float s_y[G][TILE_F];
   auto at = [](int c, int t) { return (LAYOUT == kTimeContig) ? c * kTP + t : t * kCP + c; };
+  // Partial y's of the G waves: unpadded rows, [channel][time] with each row's 4-float
+  // chunks XOR-permuted by channel (time-contiguous) so that eight consecutive lanes'
+  // float4 accesses of one step group land on distinct banks, or [time][channel]
+  // (channel-contiguous), conflict-free as it is.  Dropping the padding of the other
+  // tiles here saves 9 KB of LDS and measured ~3% faster at config 4.
+  constexpr int YT = kCPW * kT;
+  static_assert(kT / 4 >= 8, "the chunk permutation needs eight chunks per row");
+  __shared__ __attribute__((aligned(16))) float s_y[G][YT];
+  auto aty = [](int c, int t) {
+    return (LAYOUT == kTimeContig) ? c * kT + ((((t >> 2) ^ (c & 7)) << 2) | (t & 3))
+                                   : t * kCPW + c;
+  };
   __shared__ __attribute__((aligned(16))) float s_bc[G][kT][2 * SPL];
   __shared__ int s_ticket;
 
@@ -373,6 +384,10 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
       for (int k = 0; k < SPL; ++k)
         h[k] = __hip_atomic_load(cp + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // Take delivery of the carried state here: the tile loop then finds no load pending
+    // on h, so it carries no wait for one (that wait also covered the tiles' prefetches).
+#pragma unroll
+    for (int k = 0; k < SPL; ++k) asm volatile("" : "+v"(h[k]));
 
     // process(slot, tile, slot a, slot b, issue): scan tile from the first slot; with
     // issue, load tiles tile + 2 and tile + 3 into slots a and b (both free: consumed
@@ -492,10 +507,10 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
           ys[j] = acc;
         }
         if constexpr (LAYOUT == kTimeContig) {
-          *reinterpret_cast<float4*>(&s_y[g][at(lane, tt)]) = make_float4(ys[0], ys[1], ys[2], ys[3]);
+          *reinterpret_cast<float4*>(&s_y[g][aty(lane, tt)]) = make_float4(ys[0], ys[1], ys[2], ys[3]);
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) s_y[g][at(lane, tt + j)] = ys[j];
+          for (int j = 0; j < 4; ++j) s_y[g][aty(lane, tt + j)] = ys[j];
         }
       }
       __syncthreads();
@@ -513,7 +528,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
 #pragma unroll
           for (int j = 0; j < EPT; j += VW)
             part[gg][j / VW] = *reinterpret_cast<const FV*>(
-                &s_y[gg][(LAYOUT == kTimeContig) ? at(vc, vt + j) : at(vc + j, vt)]);
+                &s_y[gg][(LAYOUT == kTimeContig) ? aty(vc, vt + j) : aty(vc + j, vt)]);
 #pragma unroll
         for (int gg = 0; gg < G; ++gg)
 #pragma unroll
