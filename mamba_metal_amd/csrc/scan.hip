@@ -41,7 +41,12 @@ namespace scan {
 #define MM_SCAN_SPL16 2
 #endif
 
-constexpr int kCPW = 64;     // channels per workgroup (lanes per wave)
+// Channels per workgroup: 64 (lane = channel) or, for the chained scan at dstate <= 16,
+// 32 (each half-wave takes the 32 channels with its own states).  kCpwMin sizes what
+// depends on the count of channel blocks (flags, tickets), kCpwMax what depends on the
+// padded channel count.
+constexpr int kCpwMax = 64;
+constexpr int kCpwMin = 32;
 #ifndef MM_SCAN_KT
 #define MM_SCAN_KT 32
 #endif
@@ -89,26 +94,31 @@ enum Mode { kChained = 0, kSummary = 1, kFromSummary = 2 };
 constexpr int64_t kSplitMaxChains = 128;  // the workspace holds summaries up to this many chains
 constexpr int64_t kSplitMaxSeg = 32;      // ... of up to this many segments each
 
-// Workspace: [ctl: ticket counters + error word][flags: ncb ints][carry: ncb*G*SPL*64
-// floats][bc: packed B/C][summaries: ncb*kSplitMaxSeg*(G*SPL*64 + 64) floats, only for
-// dstate <= 16 and ncb <= kSplitMaxChains]
+// Workspace: [ctl: ticket counters + error word][flags: one int per 32-channel block]
+// [carry: batch * dim padded to 64 * G*SPL floats][bc: packed B/C][summaries:
+// ncb*kSplitMaxSeg*(G*SPL*64 + 64) floats, only for dstate <= 16 and at most
+// kSplitMaxChains 64-channel blocks].  G is the number of state groups (8 for dstate
+// <= 16, else 4); a 32-channel block uses half as many carry floats as a 64-channel one,
+// so the layout serves either channel block.
 struct WsLayout {
   size_t flags, carry, bc, sum, total;
 };
 
 inline bool split_capable(int64_t ncb, int64_t groups) { return groups == 8 && ncb <= kSplitMaxChains; }
 
+inline int64_t max_blocks(int64_t batch, int64_t dim) { return batch * ceil_div(dim, kCpwMin); }
+
 inline WsLayout ws_layout(int64_t batch, int64_t dim, int64_t groups, int64_t spl, int64_t seqlen) {
-  const int64_t ncb = batch * ceil_div(dim, kCPW);
+  const int64_t ncb = batch * ceil_div(dim, kCpwMax);
   WsLayout w;
   w.flags = 256;
-  w.carry = static_cast<size_t>(round_up(w.flags + 4 * ncb, 256));
-  w.bc = static_cast<size_t>(round_up(w.carry + 4 * ncb * groups * spl * kCPW, 256));
+  w.carry = static_cast<size_t>(round_up(w.flags + 4 * max_blocks(batch, dim), 256));
+  w.bc = static_cast<size_t>(round_up(w.carry + 4 * ncb * groups * spl * kCpwMax, 256));
   w.sum = static_cast<size_t>(
       round_up(w.bc + static_cast<size_t>(4 * batch * groups * padded_len(seqlen) * 2 * spl), 256));
   w.total = w.sum;
   if (split_capable(ncb, groups))
-    w.total += static_cast<size_t>(4 * ncb * kSplitMaxSeg * (groups * spl * kCPW + kCPW));
+    w.total += static_cast<size_t>(4 * ncb * kSplitMaxSeg * (groups * spl * kCpwMax + kCpwMax));
   return w;
 }
 
@@ -196,59 +206,67 @@ __device__ __forceinline__ float softplus_log2(float x) {
 }
 
 // ---------------------------------------------------------------------------
-template <int DT, int LAYOUT, int SPL, int G, bool VEC, int MODE>
-__global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
+template <int DT, int LAYOUT, int SPL, int G, bool VEC, int MODE, int CPW>
+__global__ __launch_bounds__(64 * G, MM_SCAN_MIN_WG) void scan_kernel(
     const Params p, const void* __restrict__ u_, const void* __restrict__ delta_,
     const void* __restrict__ z_, void* __restrict__ y_, const float* __restrict__ bc_,
     float* __restrict__ state_out_, int* __restrict__ ctl_, float* __restrict__ carry_,
     int* __restrict__ tick_, float* __restrict__ sum_) {
   using T = typename Ty<DT>::T;
-  constexpr int NT = kCPW * G;
-  constexpr int EPT = kCPW * kT / NT;  // elements per thread per tile
+  // CPW channels per workgroup: lane l takes channel l % CPW; with CPW = 32 the two
+  // half-waves take the same channels and different states (HV = 2 state groups per
+  // wave, GS = G * HV in all).
+  static_assert(CPW == 64 || CPW == 32, "channel block");
+  constexpr int HV = 64 / CPW;
+  constexpr int GS = G * HV;
+  constexpr int NT = 64 * G;
+  constexpr int EPT = CPW * kT / NT;  // elements per thread per tile
   static_assert(EPT == 8 || EPT == 4 || EPT == 2, "tile split");
   using VE = typename Vec<DT, EPT>::type;
   constexpr int VW = EPT >= 4 ? 4 : 2;  // floats per LDS vector access of the prologue/epilogue
   using FV = typename FVec<VW>::type;
   constexpr int TPC = kT / EPT;        // threads per channel (time-contiguous mapping)
-  constexpr int BCF = G * kT * 2 * SPL;  // floats of B/C per tile
+  constexpr int BCF = GS * kT * 2 * SPL;  // floats of B/C per tile
   constexpr int BCV = BCF / 4;
   constexpr int BCPT = (BCV + NT - 1) / NT;
-  constexpr int64_t SB = G * SPL * kCPW + kCPW;  // floats per segment summary
+  constexpr int64_t SB = GS * SPL * CPW + CPW;  // floats per segment summary
 
   // LDS tiles of delta2, delta2*u and the G partial y's.  Time-contiguous inputs stage
   // them channel-major ([channel][time], rows of kTP floats); channel-contiguous
   // inputs time-major ([time][channel], rows of kCP floats), so that the prologue's
   // and the epilogue's float4 accesses run along the axis each thread owns and hit
   // distinct banks either way.
-  constexpr int kCP = kCPW + 4;
-  constexpr int TILE_F = (LAYOUT == kTimeContig) ? kCPW * kTP : kT * kCP;
+  constexpr int kCP = CPW + 4;
+  constexpr int TILE_F = (LAYOUT == kTimeContig) ? CPW * kTP : kT * kCP;
   __shared__ __attribute__((aligned(16))) float s_dt[TILE_F];
   __shared__ __attribute__((aligned(16))) float s_du[TILE_F];
   auto at = [](int c, int t) { return (LAYOUT == kTimeContig) ? c * kTP + t : t * kCP + c; };
-  // Partial y's of the G waves: unpadded rows, [channel][time] with each row's 4-float
+  // Partial y's of the GS state groups: unpadded rows, [channel][time] with each row's 4-float
   // chunks XOR-permuted by channel (time-contiguous) so that eight consecutive lanes'
   // float4 accesses of one step group land on distinct banks, or [time][channel]
   // (channel-contiguous), conflict-free as it is.  Dropping the padding of the other
   // tiles here saves 9 KB of LDS and measured ~3% faster at config 4.
-  constexpr int YT = kCPW * kT;
+  constexpr int YT = CPW * kT;
   static_assert(kT / 4 >= 8, "the chunk permutation needs eight chunks per row");
-  __shared__ __attribute__((aligned(16))) float s_y[G][YT];
+  __shared__ __attribute__((aligned(16))) float s_y[GS][YT];
   auto aty = [](int c, int t) {
     return (LAYOUT == kTimeContig) ? c * kT + ((((t >> 2) ^ (c & 7)) << 2) | (t & 3))
-                                   : t * kCPW + c;
+                                   : t * CPW + c;
   };
-  __shared__ __attribute__((aligned(16))) float s_bc[G][kT][2 * SPL];
+  __shared__ __attribute__((aligned(16))) float s_bc[GS][kT][2 * SPL];
   __shared__ int s_ticket;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int g = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lch = lane & (CPW - 1);        // this lane's channel in the block
+  const int sg = (lane / CPW) * G + g;     // this lane's state group (uniform when HV = 1)
   const bool has_z = z_ != nullptr;
 
   // Element ownership for the prologue / epilogue: consecutive threads walk the
   // contiguous axis, so a wave's vector access covers whole 128-byte rows -- along
   // time (TPC threads per channel row) or along channels (CPT threads per step row).
-  constexpr int CPT = kCPW / EPT;
+  constexpr int CPT = CPW / EPT;
   const int vc = (LAYOUT == kTimeContig) ? (tid / TPC) : ((tid % CPT) * EPT);
   const int vt = (LAYOUT == kTimeContig) ? ((tid % TPC) * EPT) : (tid / CPT);
   auto ec = [&](int j) { return (LAYOUT == kTimeContig) ? vc : vc + j; };
@@ -264,7 +282,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
     const int64_t cb = unit % p.ncb;
     const int64_t seg = unit / p.ncb;
     const int64_t b = cb / p.nblk_d;
-    const int64_t d0 = (cb % p.nblk_d) * kCPW;
+    const int64_t d0 = (cb % p.nblk_d) * CPW;
     const int64_t tile0 = seg * p.seg_tiles;
     const int64_t tile1 = std::min<int64_t>(tile0 + p.seg_tiles, p.Lp / kT);
 
@@ -272,10 +290,10 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
     float Av[SPL], h[SPL];
     float dsum = 0.0f;  // kSummary: sum of delta2 over the segment (this lane's channel)
     {
-      const int64_t d = d0 + lane;
+      const int64_t d = d0 + lch;
 #pragma unroll
       for (int k = 0; k < SPL; ++k) {
-        const int64_t n = static_cast<int64_t>(g) * SPL + k;
+        const int64_t n = static_cast<int64_t>(sg) * SPL + k;
         Av[k] = (d < p.dim && n < p.dstate) ? p.A[d * p.As0 + n * p.As1] : 0.0f;
         h[k] = 0.0f;
       }
@@ -313,7 +331,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
     for (int i = 0; i < BCPT; ++i) {
       const int v = (tid + i * NT) % BCV;
       const int gg = v / (kT * 2 * SPL / 4), rest = v % (kT * 2 * SPL / 4);
-      bcb[i] = bc_ + (b * G + gg) * p.Lp * (2 * SPL) + rest * 4;
+      bcb[i] = bc_ + (b * GS + gg) * p.Lp * (2 * SPL) + rest * 4;
     }
     const int64_t dcl = (d0 + vc < p.dim) ? d0 + vc : 0;
     const T* const ub = static_cast<const T*>(u_) + b * p.us0 + dcl * p.us1;
@@ -356,10 +374,10 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
       // fold the summaries of segments 0 .. seg-1 (written by the kSummary launch)
       for (int64_t j = 0; j < seg; ++j) {
         const float* sb = sum_ + (cb * p.nseg + j) * SB;
-        const float dl = sb[G * SPL * kCPW + lane];
+        const float dl = sb[GS * SPL * CPW + lch];
 #pragma unroll
         for (int k = 0; k < SPL; ++k)
-          h[k] = __builtin_fmaf(exp2_decay<DT>(Av[k] * dl), h[k], sb[(g * kCPW + lane) * SPL + k]);
+          h[k] = __builtin_fmaf(exp2_decay<DT>(Av[k] * dl), h[k], sb[(sg * CPW + lch) * SPL + k]);
       }
     }
     if (MODE == kChained && seg > 0) {
@@ -379,7 +397,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
         }
       }
       __syncthreads();
-      float* cp = carry_ + ((cb * G + g) * kCPW + lane) * SPL;
+      float* cp = carry_ + ((cb * GS + sg) * CPW + lch) * SPL;
 #pragma unroll
       for (int k = 0; k < SPL; ++k)
         h[k] = __hip_atomic_load(cp + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -396,7 +414,7 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
                        VE& zA, float4 (&bcA)[BCPT], VE& uB, VE& dB, VE& zB, float4 (&bcB)[BCPT],
                        bool issue) __attribute__((always_inline)) {
       const int64_t t0 = tile * kT;
-      const bool full = (t0 + kT <= p.seqlen) && (d0 + kCPW <= p.dim);
+      const bool full = (t0 + kT <= p.seqlen) && (d0 + CPW <= p.dim);
 
       // ---- prologue ----
       float yskip[EPT], gate[EPT], dtv[EPT], duv[EPT];
@@ -443,25 +461,26 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
       }
       __syncthreads();
 
-      // ---- scan: lane = channel, wave = state group; LDS reads one group ahead ----
+      // ---- scan: lane = channel (mod CPW), wave and half-wave = state group; LDS reads
+      // one group ahead ----
       struct Grp {
         float4 d4, u4;
         float bc[4][2 * SPL];
       };
       auto fetch = [&](int tt, Grp& gr) {
         if constexpr (LAYOUT == kTimeContig) {
-          gr.d4 = *reinterpret_cast<const float4*>(&s_dt[at(lane, tt)]);
-          gr.u4 = *reinterpret_cast<const float4*>(&s_du[at(lane, tt)]);
+          gr.d4 = *reinterpret_cast<const float4*>(&s_dt[at(lch, tt)]);
+          gr.u4 = *reinterpret_cast<const float4*>(&s_du[at(lch, tt)]);
         } else {
-          gr.d4 = make_float4(s_dt[at(lane, tt)], s_dt[at(lane, tt + 1)], s_dt[at(lane, tt + 2)],
-                              s_dt[at(lane, tt + 3)]);
-          gr.u4 = make_float4(s_du[at(lane, tt)], s_du[at(lane, tt + 1)], s_du[at(lane, tt + 2)],
-                              s_du[at(lane, tt + 3)]);
+          gr.d4 = make_float4(s_dt[at(lch, tt)], s_dt[at(lch, tt + 1)], s_dt[at(lch, tt + 2)],
+                              s_dt[at(lch, tt + 3)]);
+          gr.u4 = make_float4(s_du[at(lch, tt)], s_du[at(lch, tt + 1)], s_du[at(lch, tt + 2)],
+                              s_du[at(lch, tt + 3)]);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int k = 0; k < 2 * SPL; ++k) gr.bc[j][k] = s_bc[g][tt + j][k];
+          for (int k = 0; k < 2 * SPL; ++k) gr.bc[j][k] = s_bc[sg][tt + j][k];
       };
       Grp cur, nxt;
       constexpr bool kPipe = SPL <= 4;
@@ -507,10 +526,10 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
           ys[j] = acc;
         }
         if constexpr (LAYOUT == kTimeContig) {
-          *reinterpret_cast<float4*>(&s_y[g][aty(lane, tt)]) = make_float4(ys[0], ys[1], ys[2], ys[3]);
+          *reinterpret_cast<float4*>(&s_y[sg][aty(lch, tt)]) = make_float4(ys[0], ys[1], ys[2], ys[3]);
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) s_y[g][aty(lane, tt + j)] = ys[j];
+          for (int j = 0; j < 4; ++j) s_y[sg][aty(lch, tt + j)] = ys[j];
         }
       }
       __syncthreads();
@@ -522,15 +541,15 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
       for (int j = 0; j < EPT; ++j) yv[j] = yskip[j];
       {
         // all G partial reads in flight before the (in-order) sum
-        FV part[G][EPT / VW];
+        FV part[GS][EPT / VW];
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg)
+        for (int gg = 0; gg < GS; ++gg)
 #pragma unroll
           for (int j = 0; j < EPT; j += VW)
             part[gg][j / VW] = *reinterpret_cast<const FV*>(
                 &s_y[gg][(LAYOUT == kTimeContig) ? aty(vc, vt + j) : aty(vc + j, vt)]);
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg)
+        for (int gg = 0; gg < GS; ++gg)
 #pragma unroll
           for (int j = 0; j < EPT; j += VW)
 #pragma unroll
@@ -566,10 +585,10 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
     if constexpr (MODE == kSummary) {
       float* sb = sum_ + (cb * p.nseg + seg) * SB;
 #pragma unroll
-      for (int k = 0; k < SPL; ++k) sb[(g * kCPW + lane) * SPL + k] = h[k];
-      if (g == 0) sb[G * SPL * kCPW + lane] = dsum;
+      for (int k = 0; k < SPL; ++k) sb[(sg * CPW + lch) * SPL + k] = h[k];
+      if (sg == 0) sb[GS * SPL * CPW + lch] = dsum;
     } else if (MODE == kChained && seg + 1 < p.nseg) {
-      float* cp = carry_ + ((cb * G + g) * kCPW + lane) * SPL;
+      float* cp = carry_ + ((cb * GS + sg) * CPW + lch) * SPL;
 #pragma unroll
       for (int k = 0; k < SPL; ++k)
         __hip_atomic_store(cp + k, h[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -583,11 +602,11 @@ __global__ __launch_bounds__(kCPW * G, MM_SCAN_MIN_WG) void scan_kernel(
         __hip_atomic_store(&ctl_[64 + cb], static_cast<int>(seg + 1), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     } else if (state_out_ != nullptr && seg + 1 == p.nseg) {
-      const int64_t d = d0 + lane;
+      const int64_t d = d0 + lch;
       if (d < p.dim) {
 #pragma unroll
         for (int k = 0; k < SPL; ++k) {
-          const int64_t n = static_cast<int64_t>(g) * SPL + k;
+          const int64_t n = static_cast<int64_t>(sg) * SPL + k;
           if (n < p.dstate) state_out_[(b * p.dim + d) * p.dstate + n] = h[k];
         }
       }
@@ -664,41 +683,73 @@ inline bool pick_split(Params& p, int64_t grid_sum, int64_t grid_main) {
   return true;
 }
 
-template <int DT, int LAYOUT, int SPL, int G, bool VEC>
-void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w) {
-  auto kern = scan_kernel<DT, LAYOUT, SPL, G, VEC, kChained>;
+// Chained launch of one channel-block width: CPW channels per workgroup, G waves.
+template <int DT, int LAYOUT, int SPL, int G, bool VEC, int CPW>
+void launch_chained(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w,
+                    int64_t resident) {
+  auto kern = scan_kernel<DT, LAYOUT, SPL, G, VEC, kChained, CPW>;
   char* ws = static_cast<char*>(a->workspace);
   int* ctl = reinterpret_cast<int*>(ws);
   float* carry = reinterpret_cast<float*>(ws + w.carry);
   const float* bc = reinterpret_cast<const float*>(ws + w.bc);
-  static DeviceCache per_cu_cache;
-  const int64_t resident =
-      static_cast<int64_t>(num_cus()) * resident_per_cu(per_cu_cache, kern, kCPW * G);
   pick_segments(p, resident);
-  if constexpr (G == 8) {
-    if (split_capable(p.ncb, G) && a->workspace_bytes >= w.total) {
-      auto ksum = scan_kernel<DT, LAYOUT, SPL, G, VEC, kSummary>;
-      auto kmain = scan_kernel<DT, LAYOUT, SPL, G, VEC, kFromSummary>;
+  const int64_t grid = std::min<int64_t>(p.nunits, resident);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(64 * G), 0, s, p, a->u,
+                     a->delta, a->z, a->y, bc, a->state_out, ctl, carry, ctl, nullptr);
+}
+
+inline void set_blocks(Params& p, int64_t batch, int cpw) {
+  p.nblk_d = ceil_div(p.dim, cpw);
+  p.ncb = batch * p.nblk_d;
+}
+
+// GS state groups of SPL states.  64-channel blocks run GS waves.  With dstate <= 16
+// (GS = 8), a shape whose 64-channel chains cannot fill the chip either splits (few
+// chains, see pick_split) or runs 32-channel blocks of 4 waves: twice the chains, and at
+// half the LDS three workgroups fit a CU.  Measured at B=8 D=1536 L=8192 (192 64-channel
+// chains for 256 CUs): 0.638 -> 0.617 ms; at B=4 D=5120 L=32768 (320 chains) 64-channel
+// blocks stay ahead by ~1%.  Results are bit-identical either way (the same per-state
+// arithmetic, the partial sums in the same order).
+template <int DT, int LAYOUT, int SPL, int GS, bool VEC>
+void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w) {
+  const int64_t cus = num_cus();
+  set_blocks(p, a->batch, 64);
+  auto kern = scan_kernel<DT, LAYOUT, SPL, GS, VEC, kChained, 64>;
+  static DeviceCache per_cu_cache;
+  const int64_t resident = cus * resident_per_cu(per_cu_cache, kern, 64 * GS);
+  if constexpr (GS == 8) {
+    if (split_capable(p.ncb, GS) && a->workspace_bytes >= w.total) {
+      char* ws = static_cast<char*>(a->workspace);
+      int* ctl = reinterpret_cast<int*>(ws);
+      float* carry = reinterpret_cast<float*>(ws + w.carry);
+      const float* bc = reinterpret_cast<const float*>(ws + w.bc);
+      auto ksum = scan_kernel<DT, LAYOUT, SPL, GS, VEC, kSummary, 64>;
+      auto kmain = scan_kernel<DT, LAYOUT, SPL, GS, VEC, kFromSummary, 64>;
       static DeviceCache sum_cache, main_cache;
-      const int64_t rs =
-          static_cast<int64_t>(num_cus()) * resident_per_cu(sum_cache, ksum, kCPW * G);
-      const int64_t rm =
-          static_cast<int64_t>(num_cus()) * resident_per_cu(main_cache, kmain, kCPW * G);
+      const int64_t rs = cus * resident_per_cu(sum_cache, ksum, 64 * GS);
+      const int64_t rm = cus * resident_per_cu(main_cache, kmain, 64 * GS);
+      pick_segments(p, resident);  // the chained estimate pick_split weighs the split against
       if (pick_split(p, rs, rm)) {
         float* sum = reinterpret_cast<float*>(ws + w.sum);
-        hipLaunchKernelGGL(ksum, dim3(static_cast<unsigned>(std::min(p.nunits, rs))), dim3(kCPW * G),
+        hipLaunchKernelGGL(ksum, dim3(static_cast<unsigned>(std::min(p.nunits, rs))), dim3(64 * GS),
                            0, s, p, a->u, a->delta, a->z, a->y, bc, a->state_out, ctl, carry,
                            ctl, sum);
-        hipLaunchKernelGGL(kmain, dim3(static_cast<unsigned>(std::min(p.nunits, rm))), dim3(kCPW * G),
+        hipLaunchKernelGGL(kmain, dim3(static_cast<unsigned>(std::min(p.nunits, rm))), dim3(64 * GS),
                            0, s, p, a->u, a->delta, a->z, a->y, bc, a->state_out, ctl, carry,
                            ctl + 2, sum);
         return;
       }
     }
+    if (p.ncb < resident) {
+      auto k32 = scan_kernel<DT, LAYOUT, SPL, GS / 2, VEC, kChained, 32>;
+      static DeviceCache c32_cache;
+      const int64_t r32 = cus * resident_per_cu(c32_cache, k32, 64 * (GS / 2));
+      set_blocks(p, a->batch, 32);
+      launch_chained<DT, LAYOUT, SPL, GS / 2, VEC, 32>(p, a, s, w, r32);
+      return;
+    }
   }
-  const int64_t grid = std::min<int64_t>(p.nunits, resident);
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(kCPW * G), 0, s, p, a->u,
-                     a->delta, a->z, a->y, bc, a->state_out, ctl, carry, ctl, nullptr);
+  launch_chained<DT, LAYOUT, SPL, GS, VEC, 64>(p, a, s, w, resident);
 }
 
 template <int DT, int LAYOUT, int SPL, int G>
@@ -796,7 +847,7 @@ int validate(const mm_scan_params* a) {
   if (!valid_dtype(a->x_dtype) || !valid_dtype(a->bc_dtype))
     return fail(MM_ERR_DTYPE, "bad dtype (x_dtype=%d bc_dtype=%d)", a->x_dtype, a->bc_dtype);
   if (a->reserved != 0) return fail(MM_ERR_LAYOUT, "reserved field must be 0");
-  const int64_t ncb = a->batch * ceil_div(a->dim, kCPW);
+  const int64_t ncb = max_blocks(a->batch, a->dim);
   if (ncb > (1LL << 30)) return fail(MM_ERR_SHAPE, "too many channel blocks (%lld)", (long long)ncb);
   return MM_OK;
 }
@@ -827,7 +878,7 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
   pick_shape(a->dstate, &groups, &spl);
   if (!shape_known(groups, spl))
     return fail(MM_ERR_DSTATE, "no scan instantiation for %d groups x %d states", groups, spl);
-  const int ept = kCPW * kT / (kCPW * groups);
+  const int ept = kT / groups;  // elements per thread per tile, either channel block
   int layout = kTimeContig, vec_ok = 0;
   choose_layout(a, ept, &layout, &vec_ok);
   const WsLayout w = ws_layout(a->batch, a->dim, groups, spl, std::max<int64_t>(a->seqlen, 1));
@@ -843,9 +894,8 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
   p.dstate = a->dstate;
   p.seqlen = a->seqlen;
   p.Lp = padded_len(a->seqlen);
-  p.nblk_d = ceil_div(a->dim, kCPW);
-  p.ncb = a->batch * p.nblk_d;
-  // seg_tiles / nseg / nunits are set at launch, from the persistent grid size.
+  // nblk_d / ncb are set at launch, from the channel block, and seg_tiles / nseg /
+  // nunits from the persistent grid size.
   p.us0 = a->u_stride[0]; p.us1 = a->u_stride[1]; p.us2 = a->u_stride[2];
   p.ds0 = a->delta_stride[0]; p.ds1 = a->delta_stride[1]; p.ds2 = a->delta_stride[2];
   if (a->z) {
@@ -862,7 +912,7 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
   p.status = a->status;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t nctl = 64 + p.ncb;
+  const int64_t nctl = 64 + max_blocks(a->batch, a->dim);
   switch (a->bc_dtype) {
     case MM_F32: launch_pack<MM_F32>(a, p.Lp, groups, spl, w, nctl, s); break;
     case MM_F16: launch_pack<MM_F16>(a, p.Lp, groups, spl, w, nctl, s); break;

@@ -109,10 +109,11 @@ def test_scan_validation_errors(lib, over, status):
 
 
 def test_workspace_size(lib):
-    # control block (256 B) + flags + carried state + packed fp32 B/C (16 states -> 8
-    # groups x 2 per lane, padded to 32-step tiles)
+    # control block (256 B) + one flag per 32-channel block + carried state (per
+    # 64-channel block) + packed fp32 B/C (16 states -> 8 groups x 2 per lane, padded to
+    # 32-step tiles)
     ncb = 4 * 5120 // 64
-    flags_end = 256 + 4 * ncb
+    flags_end = 256 + 4 * (4 * 5120 // 32)
     carry = -(-flags_end // 256) * 256
     bc = -(-(carry + 4 * ncb * 16 * 64) // 256) * 256
     assert lib.mm_selective_scan_workspace_size(4, 5120, 16, 32768) == bc + 4 * 4 * 16 * 32768 * 2

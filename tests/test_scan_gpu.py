@@ -6,7 +6,7 @@ Cases restate the reference's own scan checks, now with assertions:
   18-prefill/verify_state_out (final state)
 plus edge shapes, strided layouts, dtypes, determinism and the BASELINE
 configs (config 0 against the committed golden fixture; configs 2 and 4 at full
-size with one channel of every 64-channel block against the oracle -- channels are
+size with one channel of every 32-channel block against the oracle -- channels are
 independent, so any subset must match the oracle run on that subset alone).
 
 Tolerances (from the task's parity bar): fp32 rtol 1e-5 (atol 1e-5 for |y| ~ 0);
@@ -254,10 +254,11 @@ def test_config0_against_golden(dev):
 
 
 def _blockwise_parity(oracle_lib, dev, batch, dim, seqlen, seed):
-    """Full-size fp16 scan on the GPU; the fp64 oracle on one channel of EVERY 64-channel
-    block (a random lane per block, plus the first and last channel): each block is one
-    chain of the kernel's segment hand-offs, so every chain's hand-offs are checked.
-    Channels are independent, so a subset must match the oracle run on that subset."""
+    """Full-size fp16 scan on the GPU; the fp64 oracle on one channel of EVERY 32-channel
+    block (a random lane per block, plus the first and last channel): the kernel's
+    chains are blocks of 64 or 32 channels, each with its own segment hand-offs, so every
+    chain's hand-offs are checked.  Channels are independent, so a subset must match the
+    oracle run on that subset."""
     from mamba_metal_amd import selective_scan
     from mamba_metal_amd.selective_scan import reset_scan_status, scan_status
 
@@ -277,10 +278,10 @@ def _blockwise_parity(oracle_lib, dev, batch, dim, seqlen, seed):
     assert scan_status(dev) == 0    # every segment hand-off completed
     assert torch.isfinite(y).all()
     rng = np.random.default_rng(seed)
-    nblk = -(-dim // 64)
+    nblk = -(-dim // 32)
     checked = 0
     for b in range(batch):
-        chans = np.minimum(np.arange(nblk) * 64 + rng.integers(0, 64, nblk), dim - 1)
+        chans = np.minimum(np.arange(nblk) * 32 + rng.integers(0, 32, nblk), dim - 1)
         chans = np.unique(np.concatenate([chans, [0, dim - 1]]))
         idx = torch.as_tensor(chans, device=dev)
         pick = lambda t: t[b:b + 1].index_select(1, idx).float().cpu().numpy()
