@@ -253,7 +253,11 @@ __global__ __launch_bounds__(64 * G, MM_SCAN_MIN_WG) void scan_kernel(
     return (LAYOUT == kTimeContig) ? c * kT + ((((t >> 2) ^ (c & 7)) << 2) | (t & 3))
                                    : t * CPW + c;
   };
-  __shared__ __attribute__((aligned(16))) float s_bc[GS][kT][2 * SPL];
+  // B/C of the tile, one row of kT steps x (SPL B, SPL C) per state group.  A 32-channel
+  // block's half-waves read two groups G rows apart in one instruction: the 4-float pad
+  // puts those rows on different banks.
+  constexpr int BCR = kT * 2 * SPL + 4;
+  __shared__ __attribute__((aligned(16))) float s_bc[GS][BCR];
   __shared__ int s_ticket;
 
   const int tid = threadIdx.x;
@@ -453,7 +457,10 @@ __global__ __launch_bounds__(64 * G, MM_SCAN_MIN_WG) void scan_kernel(
 #pragma unroll
       for (int i = 0; i < BCPT; ++i) {
         const int v = tid + i * NT;
-        if (v < BCV) reinterpret_cast<float4*>(&s_bc[0][0][0])[v] = rbc[i];
+        if (v < BCV) {
+          constexpr int VPG = kT * 2 * SPL / 4;  // float4s per state group
+          *reinterpret_cast<float4*>(&s_bc[v / VPG][(v % VPG) * 4]) = rbc[i];
+        }
       }
       if (issue) {  // in flight during the next two tiles' scans
         load_raw(uA, dA, zA, bcA, t0 + 2 * kT);
@@ -480,7 +487,7 @@ __global__ __launch_bounds__(64 * G, MM_SCAN_MIN_WG) void scan_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int k = 0; k < 2 * SPL; ++k) gr.bc[j][k] = s_bc[sg][tt + j][k];
+          for (int k = 0; k < 2 * SPL; ++k) gr.bc[j][k] = s_bc[sg][(tt + j) * 2 * SPL + k];
       };
       Grp cur, nxt;
       constexpr bool kPipe = SPL <= 4;
@@ -703,21 +710,20 @@ inline void set_blocks(Params& p, int64_t batch, int cpw) {
   p.ncb = batch * p.nblk_d;
 }
 
-// GS state groups of SPL states.  64-channel blocks run GS waves.  With dstate <= 16
-// (GS = 8), a shape whose 64-channel chains cannot fill the chip either splits (few
-// chains, see pick_split) or runs 32-channel blocks of 4 waves: twice the chains, and at
-// half the LDS three workgroups fit a CU.  Measured at B=8 D=1536 L=8192 (192 64-channel
-// chains for 256 CUs): 0.638 -> 0.617 ms; at B=4 D=5120 L=32768 (320 chains) 64-channel
-// blocks stay ahead by ~1%.  Results are bit-identical either way (the same per-state
-// arithmetic, the partial sums in the same order).
+// GS state groups of SPL states.  dstate > 16 (GS = 4): the chained scan on 64-channel
+// blocks of 4 waves.  dstate <= 16 (GS = 8): the split scan on 64-channel blocks of 8
+// waves where it pays (few chains, see pick_split), else the chained scan on 32-channel
+// blocks of 4 waves.  A 32-channel block needs half the LDS of a 64-channel one, so three
+// fit a CU (three independent workgroups, one wave per SIMD each, instead of one
+// workgroup with two waves per SIMD in lockstep through its barriers), and there are twice
+// as many chains.  Measured against 64-channel blocks: 3.17 -> 3.05-3.11 ms at B=4 D=5120
+// L=32768 (VALU busy 68% -> 73%), 0.640 -> 0.606 ms at B=8 D=1536 L=8192, with
+// bit-identical results (the same per-state arithmetic, the partial sums in the same order).
 template <int DT, int LAYOUT, int SPL, int GS, bool VEC>
 void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w) {
   const int64_t cus = num_cus();
-  set_blocks(p, a->batch, 64);
-  auto kern = scan_kernel<DT, LAYOUT, SPL, GS, VEC, kChained, 64>;
-  static DeviceCache per_cu_cache;
-  const int64_t resident = cus * resident_per_cu(per_cu_cache, kern, 64 * GS);
   if constexpr (GS == 8) {
+    set_blocks(p, a->batch, 64);
     if (split_capable(p.ncb, GS) && a->workspace_bytes >= w.total) {
       char* ws = static_cast<char*>(a->workspace);
       int* ctl = reinterpret_cast<int*>(ws);
@@ -728,7 +734,9 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
       static DeviceCache sum_cache, main_cache;
       const int64_t rs = cus * resident_per_cu(sum_cache, ksum, 64 * GS);
       const int64_t rm = cus * resident_per_cu(main_cache, kmain, 64 * GS);
-      pick_segments(p, resident);  // the chained estimate pick_split weighs the split against
+      // the chained estimate pick_split weighs the split against (kFromSummary has the
+      // chained kernel's footprint)
+      pick_segments(p, rm);
       if (pick_split(p, rs, rm)) {
         float* sum = reinterpret_cast<float*>(ws + w.sum);
         hipLaunchKernelGGL(ksum, dim3(static_cast<unsigned>(std::min(p.nunits, rs))), dim3(64 * GS),
@@ -740,16 +748,27 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
         return;
       }
     }
-    if (p.ncb < resident) {
-      auto k32 = scan_kernel<DT, LAYOUT, SPL, GS / 2, VEC, kChained, 32>;
-      static DeviceCache c32_cache;
-      const int64_t r32 = cus * resident_per_cu(c32_cache, k32, 64 * (GS / 2));
-      set_blocks(p, a->batch, 32);
-      launch_chained<DT, LAYOUT, SPL, GS / 2, VEC, 32>(p, a, s, w, r32);
-      return;
-    }
+    auto k32 = scan_kernel<DT, LAYOUT, SPL, GS / 2, VEC, kChained, 32>;
+    static DeviceCache c32_cache;
+    int64_t r32 = cus * resident_per_cu(c32_cache, k32, 64 * (GS / 2));
+    set_blocks(p, a->batch, 32);
+    // Persistent grid size, measured on 256 CUs (three workgroups fit a CU): with two to
+    // four chains per CU, two workgroups per CU (B=4 D=5120 L=32768, 640 chains: 2.88 ms
+    // at 512 workgroups, 3.07 at 768, 3.0-3.2 at 576; B=16 D=1536 L=4096, 768 chains:
+    // 0.464 vs 0.500 ms); otherwise every resident slot -- with more chains the tickets
+    // keep three per CU evenly busy (B=8..64 x D=5120, 1280-10240 chains: 1.30-1.32 ms at
+    // 768 vs 1.46-1.47 at 512), with fewer the chains' segment order is the critical path
+    // and spare workgroups take the next segments early (B=8 D=1536 L=8192: 0.605 ms at
+    // 768, 0.627 at 512).
+    if (p.ncb >= 2 * cus && p.ncb < 4 * cus && r32 > 2 * cus) r32 = 2 * cus;
+    launch_chained<DT, LAYOUT, SPL, GS / 2, VEC, 32>(p, a, s, w, r32);
+  } else {
+    auto kern = scan_kernel<DT, LAYOUT, SPL, GS, VEC, kChained, 64>;
+    static DeviceCache per_cu_cache;
+    const int64_t resident = cus * resident_per_cu(per_cu_cache, kern, 64 * GS);
+    set_blocks(p, a->batch, 64);
+    launch_chained<DT, LAYOUT, SPL, GS, VEC, 64>(p, a, s, w, resident);
   }
-  launch_chained<DT, LAYOUT, SPL, GS, VEC, 64>(p, a, s, w, resident);
 }
 
 template <int DT, int LAYOUT, int SPL, int G>
