@@ -89,9 +89,11 @@ struct Params {
 // sum of delta2 per channel; kFromSummary then starts segment s from the state folded
 // out of the summaries of segments 0 .. s-1 (h = exp2(A * sum delta2) * h + h_local),
 // so no unit waits.  The split costs a second pass over the inputs; it pays when the
-// chains (batch * dim / 64) are far fewer than the workgroups the chip holds.
+// chains (channel blocks) are far fewer than the workgroups the chip holds.
 enum Mode { kChained = 0, kSummary = 1, kFromSummary = 2 };
-constexpr int64_t kSplitMaxChains = 128;  // the workspace holds summaries up to this many chains
+// The workspace holds summaries for up to this many 64-channel blocks (the same bytes as
+// twice as many 32-channel blocks).
+constexpr int64_t kSplitMaxChains = 128;
 constexpr int64_t kSplitMaxSeg = 32;      // ... of up to this many segments each
 
 // Workspace: [ctl: ticket counters + error word][flags: one int per 32-channel block]
@@ -711,9 +713,8 @@ inline void set_blocks(Params& p, int64_t batch, int cpw) {
 }
 
 // GS state groups of SPL states.  dstate > 16 (GS = 4): the chained scan on 64-channel
-// blocks of 4 waves.  dstate <= 16 (GS = 8): the split scan on 64-channel blocks of 8
-// waves where it pays (few chains, see pick_split), else the chained scan on 32-channel
-// blocks of 4 waves.  A 32-channel block needs half the LDS of a 64-channel one, so three
+// blocks of 4 waves.  dstate <= 16 (GS = 8): 32-channel blocks of 4 waves, split where it
+// pays (few chains, see pick_split), else chained.  A 32-channel block needs half the LDS of a 64-channel one, so three
 // fit a CU (three independent workgroups, one wave per SIMD each, instead of one
 // workgroup with two waves per SIMD in lockstep through its barriers), and there are twice
 // as many chains.  Measured against 64-channel blocks: 3.17 -> 3.05-3.11 ms at B=4 D=5120
@@ -723,35 +724,35 @@ template <int DT, int LAYOUT, int SPL, int GS, bool VEC>
 void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w) {
   const int64_t cus = num_cus();
   if constexpr (GS == 8) {
+    constexpr int G = GS / 2;  // waves of a 32-channel block
     set_blocks(p, a->batch, 64);
-    if (split_capable(p.ncb, GS) && a->workspace_bytes >= w.total) {
+    const bool split_ok = split_capable(p.ncb, GS) && a->workspace_bytes >= w.total;
+    auto k32 = scan_kernel<DT, LAYOUT, SPL, G, VEC, kChained, 32>;
+    static DeviceCache c32_cache;
+    int64_t r32 = cus * resident_per_cu(c32_cache, k32, 64 * G);
+    set_blocks(p, a->batch, 32);
+    if (split_ok) {
       char* ws = static_cast<char*>(a->workspace);
       int* ctl = reinterpret_cast<int*>(ws);
       float* carry = reinterpret_cast<float*>(ws + w.carry);
       const float* bc = reinterpret_cast<const float*>(ws + w.bc);
-      auto ksum = scan_kernel<DT, LAYOUT, SPL, GS, VEC, kSummary, 64>;
-      auto kmain = scan_kernel<DT, LAYOUT, SPL, GS, VEC, kFromSummary, 64>;
+      auto ksum = scan_kernel<DT, LAYOUT, SPL, G, VEC, kSummary, 32>;
+      auto kmain = scan_kernel<DT, LAYOUT, SPL, G, VEC, kFromSummary, 32>;
       static DeviceCache sum_cache, main_cache;
-      const int64_t rs = cus * resident_per_cu(sum_cache, ksum, 64 * GS);
-      const int64_t rm = cus * resident_per_cu(main_cache, kmain, 64 * GS);
-      // the chained estimate pick_split weighs the split against (kFromSummary has the
-      // chained kernel's footprint)
-      pick_segments(p, rm);
+      const int64_t rs = cus * resident_per_cu(sum_cache, ksum, 64 * G);
+      const int64_t rm = cus * resident_per_cu(main_cache, kmain, 64 * G);
+      pick_segments(p, r32);  // the chained estimate pick_split weighs the split against
       if (pick_split(p, rs, rm)) {
         float* sum = reinterpret_cast<float*>(ws + w.sum);
-        hipLaunchKernelGGL(ksum, dim3(static_cast<unsigned>(std::min(p.nunits, rs))), dim3(64 * GS),
+        hipLaunchKernelGGL(ksum, dim3(static_cast<unsigned>(std::min(p.nunits, rs))), dim3(64 * G),
                            0, s, p, a->u, a->delta, a->z, a->y, bc, a->state_out, ctl, carry,
                            ctl, sum);
-        hipLaunchKernelGGL(kmain, dim3(static_cast<unsigned>(std::min(p.nunits, rm))), dim3(64 * GS),
+        hipLaunchKernelGGL(kmain, dim3(static_cast<unsigned>(std::min(p.nunits, rm))), dim3(64 * G),
                            0, s, p, a->u, a->delta, a->z, a->y, bc, a->state_out, ctl, carry,
                            ctl + 2, sum);
         return;
       }
     }
-    auto k32 = scan_kernel<DT, LAYOUT, SPL, GS / 2, VEC, kChained, 32>;
-    static DeviceCache c32_cache;
-    int64_t r32 = cus * resident_per_cu(c32_cache, k32, 64 * (GS / 2));
-    set_blocks(p, a->batch, 32);
     // Persistent grid size, measured on 256 CUs (three workgroups fit a CU): with two to
     // four chains per CU, two workgroups per CU (B=4 D=5120 L=32768, 640 chains: 2.88 ms
     // at 512 workgroups, 3.07 at 768, 3.0-3.2 at 576; B=16 D=1536 L=4096, 768 chains:
