@@ -94,12 +94,19 @@ enum Mode { kChained = 0, kSummary = 1, kFromSummary = 2 };
 // The workspace holds summaries for up to this many 64-channel blocks (the same bytes as
 // twice as many 32-channel blocks).
 constexpr int64_t kSplitMaxChains = 128;
-constexpr int64_t kSplitMaxSeg = 32;      // ... of up to this many segments each
+// Segment summaries the workspace holds (per 64-channel block and segment): 32 segments
+// for each of kSplitMaxChains blocks, and up to 256 segments per block when there are fewer
+// blocks -- a lone chain (the reference's B=1 D=16 benchmark) then splits finely enough
+// that both passes are short.
+constexpr int64_t kSplitSummaries = kSplitMaxChains * 32;
+inline int64_t split_max_seg(int64_t ncb64) {
+  return std::min<int64_t>(256, kSplitSummaries / std::max<int64_t>(ncb64, 1));
+}
 
 // Workspace: [ctl: ticket counters + error word][flags: one int per 32-channel block]
 // [carry: batch * dim padded to 64 * G*SPL floats][bc: packed B/C][summaries:
-// ncb*kSplitMaxSeg*(G*SPL*64 + 64) floats, only for dstate <= 16 and at most
-// kSplitMaxChains 64-channel blocks].  G is the number of state groups (8 for dstate
+// ncb*split_max_seg(ncb)*(G*SPL*64 + 64) floats for ncb 64-channel blocks, only for
+// dstate <= 16 and at most kSplitMaxChains blocks].  G is the number of state groups (8 for dstate
 // <= 16, else 4); a 32-channel block uses half as many carry floats as a 64-channel one,
 // so the layout serves either channel block.
 struct WsLayout {
@@ -120,7 +127,7 @@ inline WsLayout ws_layout(int64_t batch, int64_t dim, int64_t groups, int64_t sp
       round_up(w.bc + static_cast<size_t>(4 * batch * groups * padded_len(seqlen) * 2 * spl), 256));
   w.total = w.sum;
   if (split_capable(ncb, groups))
-    w.total += static_cast<size_t>(4 * ncb * kSplitMaxSeg * (groups * spl * kCpwMax + kCpwMax));
+    w.total += static_cast<size_t>(4 * ncb * split_max_seg(ncb) * (groups * spl * kCpwMax + kCpwMax));
   return w;
 }
 
@@ -377,13 +384,28 @@ __global__ __launch_bounds__(64 * G, MM_SCAN_MIN_WG) void scan_kernel(
 
     // ---- carried state from the previous segment of this chain ----
     if (MODE == kFromSummary && seg > 0) {
-      // fold the summaries of segments 0 .. seg-1 (written by the kSummary launch)
-      for (int64_t j = 0; j < seg; ++j) {
-        const float* sb = sum_ + (cb * p.nseg + j) * SB;
-        const float dl = sb[GS * SPL * CPW + lch];
+      // Fold the summaries of segments 0 .. seg-1 (written by the kSummary launch), in
+      // order.  Their loads are independent of the fold, so they are issued kFold
+      // segments at a time (clamped to segment seg-1, whose extra copies are not
+      // folded): one memory round trip per kFold segments instead of one per segment.
+      constexpr int kFold = 8;
+      for (int64_t j0 = 0; j0 < seg; j0 += kFold) {
+        float dlv[kFold], hlv[kFold][SPL];
 #pragma unroll
-        for (int k = 0; k < SPL; ++k)
-          h[k] = __builtin_fmaf(exp2_decay<DT>(Av[k] * dl), h[k], sb[(sg * CPW + lch) * SPL + k]);
+        for (int q = 0; q < kFold; ++q) {
+          const int64_t j = j0 + q < seg ? j0 + q : seg - 1;
+          const float* sb = sum_ + (cb * p.nseg + j) * SB;
+          dlv[q] = sb[GS * SPL * CPW + lch];
+#pragma unroll
+          for (int k = 0; k < SPL; ++k) hlv[q][k] = sb[(sg * CPW + lch) * SPL + k];
+        }
+#pragma unroll
+        for (int q = 0; q < kFold; ++q) {
+          if (j0 + q >= seg) break;
+#pragma unroll
+          for (int k = 0; k < SPL; ++k)
+            h[k] = __builtin_fmaf(exp2_decay<DT>(Av[k] * dlv[q]), h[k], hlv[q][k]);
+        }
       }
     }
     if (MODE == kChained && seg > 0) {
@@ -671,13 +693,13 @@ inline void pick_segments(Params& p, int64_t grid) {
 // estimate; the split one is ceil(units / grid) rounds of the summary pass (~3/4 of a
 // tile per tile: no epilogue, no z) plus as many of the main pass, each unit with one
 // tile of overhead, plus two tiles for the second launch.  Segments of the split are
-// whole groups of four tiles, at most kSplitMaxSeg per chain.
-inline bool pick_split(Params& p, int64_t grid_sum, int64_t grid_main) {
+// whole groups of four tiles, at most max_seg per chain.
+inline bool pick_split(Params& p, int64_t grid_sum, int64_t grid_main, int64_t max_seg) {
   const int64_t ntiles = p.Lp / kT;
   const int64_t chained4 = 4 * ceil_div(p.nunits, std::max<int64_t>(1, std::min(grid_main, p.ncb))) *
                            (p.seg_tiles + 1);
   int64_t best = INT64_MAX, best_st = 0;
-  for (int64_t n = 2; n <= kSplitMaxSeg; ++n) {
+  for (int64_t n = 2; n <= max_seg; ++n) {
     const int64_t st = round_up(ceil_div(ntiles, n), kTGroup);
     const int64_t ns = ceil_div(ntiles, st);
     if (ns < 2) continue;
@@ -726,7 +748,8 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
   if constexpr (GS == 8) {
     constexpr int G = GS / 2;  // waves of a 32-channel block
     set_blocks(p, a->batch, 64);
-    const bool split_ok = split_capable(p.ncb, GS) && a->workspace_bytes >= w.total;
+    const int64_t ncb64 = p.ncb;
+    const bool split_ok = split_capable(ncb64, GS) && a->workspace_bytes >= w.total;
     auto k32 = scan_kernel<DT, LAYOUT, SPL, G, VEC, kChained, 32>;
     static DeviceCache c32_cache;
     int64_t r32 = cus * resident_per_cu(c32_cache, k32, 64 * G);
@@ -742,7 +765,8 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
       const int64_t rs = cus * resident_per_cu(sum_cache, ksum, 64 * G);
       const int64_t rm = cus * resident_per_cu(main_cache, kmain, 64 * G);
       pick_segments(p, r32);  // the chained estimate pick_split weighs the split against
-      if (pick_split(p, rs, rm)) {
+      // 32-channel summaries take at most the bytes of the 64-channel ones
+      if (pick_split(p, rs, rm, split_max_seg(ncb64))) {
         float* sum = reinterpret_cast<float*>(ws + w.sum);
         hipLaunchKernelGGL(ksum, dim3(static_cast<unsigned>(std::min(p.nunits, rs))), dim3(64 * G),
                            0, s, p, a->u, a->delta, a->z, a->y, bc, a->state_out, ctl, carry,

@@ -122,10 +122,14 @@ def test_workspace_size(lib):
     # more than 128 channel blocks: no summary region; 64 states pack more B/C per step
     assert lib.mm_selective_scan_workspace_size(3, 5120, 64, 100) > \
         lib.mm_selective_scan_workspace_size(3, 5120, 16, 100)
-    # <= 128 channel blocks and dstate <= 16: + segment summaries for the split scan,
-    # 32 segments x (8 groups x 2 states x 64 lanes + 64 delta sums) fp32 per block
+    # <= 128 64-channel blocks and dstate <= 16: + segment summaries for the split scan,
+    # min(256, 4096 / blocks) segments x (8 groups x 2 states x 64 lanes + 64 delta sums)
+    # fp32 per block
     small = 20992  # ctl/flags 512 + carry 4096 + B/C 16384 (one 128-step padded row)
-    assert lib.mm_selective_scan_workspace_size(1, 64, 16, 100) == small + 4 * 32 * (16 * 64 + 64)
+    assert lib.mm_selective_scan_workspace_size(1, 64, 16, 100) == small + 4 * 256 * (16 * 64 + 64)
+    # 128 blocks: 32 segments each (ctl + 256 flags 1280 B, carry 524288, B/C 2097152)
+    assert lib.mm_selective_scan_workspace_size(128, 64, 16, 100) == \
+        1280 + 524288 + 2097152 + 4 * 128 * 32 * (16 * 64 + 64)
 
 
 def test_strided_null_params(lib):
