@@ -77,7 +77,8 @@ const char* mm_status_name(int status);
 
 /* Device workspace (bytes) the scan needs: B/C repacked as fp32 for the kernel,
  * the per-(channel block) state carried between time segments, and the work-queue
- * counter and flags.  Depends on dim through the number of 64-channel blocks.
+ * counter and flags.  Depends on dim through the number of 32- and 64-channel blocks,
+ * and for few blocks (dstate <= 16) includes the split scan's segment summaries.
  * The int32 at byte offset 4 of the workspace is a status word, cleared by every call:
  * nonzero afterwards means a segment gave up waiting for its predecessor's carried
  * state (a bounded wait that is not expected to expire) and y is not valid.  Read it
