@@ -338,6 +338,35 @@ def test_split_mode_matches_chained(oracle_lib, dev):
     assert (y0 - ys[..., -128:]).abs().max().item() > 0.1
 
 
+def test_split_lone_chain_many_segments(oracle_lib, dev):
+    """The reference's benchmark shape (B=1, D=16, N=16, L=32768; one chain) splits into
+    up to 256 segments, so the last segment folds 255 summaries.  Slow decay (A in
+    [-2, -0.001], delta <= 0.1) keeps states alive across many segments; fp32 bar against
+    the fp64 oracle, y and final state."""
+    from mamba_metal_amd import selective_scan
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(12)
+    batch, dim, n, L = 1, 16, 16, 32768
+    u = torch.randn((batch, dim, L), generator=g, device=dev)
+    d = torch.rand((batch, dim, L), generator=g, device=dev) * 0.09 + 0.01
+    B = torch.randn((batch, n, L), generator=g, device=dev)
+    C = torch.randn((batch, n, L), generator=g, device=dev)
+    A = -(torch.rand((dim, n), generator=g, device=dev) * 1.999 + 0.001)
+    y, h = selective_scan(u, d, A, B, C, return_state=True)
+    torch.cuda.synchronize()
+    cpu = lambda t: t.cpu().numpy()
+    yo, ho = oracle_lib.selective_scan(cpu(u), cpu(d), cpu(A), cpu(B), cpu(C))
+    assert_close(cpu(y), yo, 1e-5, 1e-5, "lone chain y")
+    assert_close(cpu(h), ho, 1e-5, 1e-5, "lone chain state")
+
+
+def test_split_few_chains_full_length(oracle_lib, dev):
+    """B=1, D=5120, L=32768 fp16 (80 64-channel blocks: the split path with up to 51
+    segments per chain), one channel of every 32-channel block against the oracle."""
+    _blockwise_parity(oracle_lib, dev, 1, 5120, 32768, seed=5)
+
+
 def test_config2_full_size_every_block(oracle_lib, dev):
     _blockwise_parity(oracle_lib, dev, 8, 1536, 8192, seed=2)
 
