@@ -6,24 +6,27 @@
 // mamba_metal/selective_scan.py:23-80.  The decomposition is this library's own.
 //
 // Work decomposition
-//   * A workgroup owns a block of 64 channels (one per lane) of one batch row and
-//     G waves; wave g owns states [g*SPL, (g+1)*SPL) of every channel (G*SPL >= dstate).
-//     Each lane walks time SEQUENTIALLY with its SPL states in fp32 registers: the
-//     recurrence costs one exp2 and four VALU ops per (channel, state, step), with no
-//     parallel-scan overhead.
+//   * A workgroup owns a block of channels of one batch row.  dstate <= 16: 32 channels
+//     and 4 waves; lane l takes channel l % 32 and the two half-waves of wave g take
+//     state groups g and g + 4 of SPL = 2 states (8 groups cover 16 states).  dstate >
+//     16: 64 channels (one per lane) and 4 waves of SPL = 8 or 16 states.  Each lane
+//     walks time SEQUENTIALLY with its SPL states in fp32 registers: the recurrence
+//     costs one exp2 and four VALU ops per (channel, state, step), with no parallel-scan
+//     overhead.
 //   * Time is cut into segments.  Work units = (channel block, segment), numbered
-//     segment-major.  A persistent grid (one or two workgroups per CU) claims units
-//     from an atomic ticket counter; a unit waits for its predecessor segment's flag,
-//     reads the carried fp32 state, scans its segment, writes the state and raises its
-//     own flag.  Every predecessor was claimed earlier by a resident workgroup, so the
-//     wait always ends; the spin is bounded anyway.  This balances 320 channel blocks
-//     (config 4) over 256 CUs, which a one-block-per-workgroup grid cannot.
-//   * Per 32-step tile the workgroup runs a prologue over the 64 x 32 (channel, time)
-//     elements -- coalesced vector loads of u, delta, z along whichever axis is
-//     contiguous, softplus, delta*u, D*u, SiLU(z) -- and stages delta', delta'*u and
-//     the tile's B/C (packed fp32 by a small kernel) in LDS; the G waves scan with
-//     LDS reads software-pipelined one 4-step group ahead; the epilogue sums the G
-//     partial y's, adds D*u, gates and stores with vector stores.  The next tile's
+//     segment-major.  A persistent grid (two or three workgroups per CU for 32-channel
+//     blocks) claims units from an atomic ticket counter; a unit waits for its
+//     predecessor segment's flag, reads the carried fp32 state, scans its segment,
+//     writes the state and raises its own flag.  Every predecessor was claimed earlier
+//     by a resident workgroup, so the wait always ends; the spin is bounded anyway.
+//     Segment-major units balance any number of chains over the CUs.  With few chains
+//     the split mode (see Mode) replaces the hand-off by segment summaries.
+//   * Per 32-step tile the workgroup runs a prologue over its (channel, time) elements
+//     -- coalesced vector loads of u, delta, z along whichever axis is contiguous,
+//     softplus, delta*u, D*u, SiLU(z) -- and stages delta', delta'*u and the tile's B/C
+//     (packed fp32 by a small kernel) in LDS; the waves scan with LDS reads
+//     software-pipelined one 4-step group ahead; the epilogue sums the state groups'
+//     partial y's, adds D*u, gates and stores with vector stores.  The next tiles'
 //     global loads are issued before the scan so HBM latency hides under VALU work.
 //   * Exponentials run in the log2 domain: delta2 = delta' * log2(e) so exp(delta'*A)
 //     = exp2(delta2 * A); the packed B carries the matching factor ln(2).
