@@ -94,14 +94,14 @@ struct Params {
 // so no unit waits.  The split costs a second pass over the inputs; it pays when the
 // chains (channel blocks) are far fewer than the workgroups the chip holds.
 enum Mode { kChained = 0, kSummary = 1, kFromSummary = 2 };
-// The workspace holds summaries for up to this many 64-channel blocks (the same bytes as
-// twice as many 32-channel blocks).
+// Split mode for up to this many 64-channel blocks (see split_capable); summaries of 32-
+// channel blocks take the same bytes as those of half as many 64-channel blocks.
 constexpr int64_t kSplitMaxChains = 128;
-// Segment summaries the workspace holds (per 64-channel block and segment): 32 segments
-// for each of kSplitMaxChains blocks, and up to 256 segments per block when there are fewer
-// blocks -- a lone chain (the reference's B=1 D=16 benchmark) then splits finely enough
-// that both passes are short.
-constexpr int64_t kSplitSummaries = kSplitMaxChains * 32;
+// Segment summaries the workspace holds (per 64-channel block and segment): 4096 in all --
+// 32 segments for each of 128 blocks, 16 for 256, and up to 256 segments per block when
+// there are fewer blocks (a lone chain, the reference's B=1 D=16 benchmark, then splits
+// finely enough that both passes are short).
+constexpr int64_t kSplitSummaries = 128 * 32;
 inline int64_t split_max_seg(int64_t ncb64) {
   return std::min<int64_t>(256, kSplitSummaries / std::max<int64_t>(ncb64, 1));
 }
@@ -116,7 +116,17 @@ struct WsLayout {
   size_t flags, carry, bc, sum, total;
 };
 
-inline bool split_capable(int64_t ncb, int64_t groups) { return groups == 8 && ncb <= kSplitMaxChains; }
+// The split pays for at most kSplitMaxChains 64-channel blocks, and up to twice that for
+// long sequences (>= kSplitLongTiles tiles), where a chain's walk dominates: measured at
+// B=2 D=5120 (160 blocks) L=32768 2.33 -> 2.14 ms, but at L=8192 (B=8 D=1536, 192 blocks)
+// 0.65 -> 0.79 ms and at L=4096 (B=3 D=5120, 240 blocks) 0.36 -> 0.43 ms, where the second
+// pass over the inputs costs more than the chain walk it shortens.
+constexpr int64_t kSplitLongTiles = 512;
+inline bool split_capable(int64_t ncb, int64_t groups, int64_t seqlen) {
+  if (groups != 8) return false;
+  return ncb <= kSplitMaxChains ||
+         (ncb <= 2 * kSplitMaxChains && padded_len(seqlen) / kT >= kSplitLongTiles);
+}
 
 inline int64_t max_blocks(int64_t batch, int64_t dim) { return batch * ceil_div(dim, kCpwMin); }
 
@@ -129,7 +139,7 @@ inline WsLayout ws_layout(int64_t batch, int64_t dim, int64_t groups, int64_t sp
   w.sum = static_cast<size_t>(
       round_up(w.bc + static_cast<size_t>(4 * batch * groups * padded_len(seqlen) * 2 * spl), 256));
   w.total = w.sum;
-  if (split_capable(ncb, groups))
+  if (split_capable(ncb, groups, seqlen))
     w.total += static_cast<size_t>(4 * ncb * split_max_seg(ncb) * (groups * spl * kCpwMax + kCpwMax));
   return w;
 }
@@ -752,7 +762,7 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
     constexpr int G = GS / 2;  // waves of a 32-channel block
     set_blocks(p, a->batch, 64);
     const int64_t ncb64 = p.ncb;
-    const bool split_ok = split_capable(ncb64, GS) && a->workspace_bytes >= w.total;
+    const bool split_ok = split_capable(ncb64, GS, a->seqlen) && a->workspace_bytes >= w.total;
     auto k32 = scan_kernel<DT, LAYOUT, SPL, G, VEC, kChained, 32>;
     static DeviceCache c32_cache;
     int64_t r32 = cus * resident_per_cu(c32_cache, k32, 64 * G);

@@ -130,6 +130,19 @@ def test_workspace_size(lib):
     # 128 blocks: 32 segments each (ctl + 256 flags 1280 B, carry 524288, B/C 2097152)
     assert lib.mm_selective_scan_workspace_size(128, 64, 16, 100) == \
         1280 + 524288 + 2097152 + 4 * 128 * 32 * (16 * 64 + 64)
+    # 129..256 blocks: summaries only for sequences of >= 512 tiles (16384 steps):
+    # 2 x 5120 = 160 blocks, 4096 // 160 = 25 segments each
+    def base(batch, dim, L):
+        up = lambda v, a: -(-v // a) * a
+        carry = up(256 + 4 * batch * (-(-dim // 32)), 256)
+        bc = up(carry + 4 * batch * (-(-dim // 64)) * 16 * 64, 256)
+        return up(bc + 4 * batch * 8 * up(L, 128) * 4, 256)
+    assert lib.mm_selective_scan_workspace_size(2, 5120, 16, 16384) == \
+        base(2, 5120, 16384) + 4 * 160 * 25 * (16 * 64 + 64)
+    assert lib.mm_selective_scan_workspace_size(2, 5120, 16, 16256) == base(2, 5120, 16256)
+    assert lib.mm_selective_scan_workspace_size(3, 5120, 16, 32768) == base(3, 5120, 32768) + \
+        4 * 240 * (4096 // 240) * (16 * 64 + 64)
+    assert lib.mm_selective_scan_workspace_size(5, 5120, 16, 32768) == base(5, 5120, 32768)
 
 
 def test_strided_null_params(lib):

@@ -383,6 +383,13 @@ def test_split_few_chains_full_length(oracle_lib, dev):
     _blockwise_parity(oracle_lib, dev, 1, 5120, 32768, seed=5)
 
 
+def test_split_long_sequence_160_blocks(oracle_lib, dev):
+    """B=2, D=5120, L=32768 fp16: 160 64-channel blocks take the split path only because
+    the sequence is long (25 segment summaries per block), one channel of every 32-channel
+    block against the oracle."""
+    _blockwise_parity(oracle_lib, dev, 2, 5120, 32768, seed=6)
+
+
 def test_config2_full_size_every_block(oracle_lib, dev):
     _blockwise_parity(oracle_lib, dev, 8, 1536, 8192, seed=2)
 
