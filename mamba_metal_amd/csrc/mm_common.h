@@ -40,7 +40,10 @@ struct DeviceCache {
 template <typename F>
 int device_cached(DeviceCache& c, F compute, int fallback) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return compute();
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    const int x = compute();  // uncached, same fallback
+    return x < 1 ? fallback : x;
+  }
   int x = c.v[dev].load(std::memory_order_relaxed);
   if (x == 0) {
     x = compute();
