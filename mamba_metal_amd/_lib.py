@@ -10,6 +10,7 @@ mapped.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -176,8 +177,23 @@ def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device) -> int:
+    """The raw HIP stream handle of ``device``'s current stream."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index)
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def on_device(device: torch.device):
+    """Context for a library call on ``device``: switches the current device only when it
+    differs (entering ``torch.cuda.device`` costs microseconds per call, which adds up over
+    the dozens of calls of a model prefill)."""
+    if device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 def require_cuda(*tensors) -> torch.device:

@@ -69,7 +69,7 @@ def pair_scan(a, b, n=None):
     a_out = torch.empty_like(a)
     h_out = torch.empty_like(b)
     if n:
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             st = lib.mm_pair_scan(a.data_ptr(), b.data_ptr(), a_out.data_ptr(), h_out.data_ptr(),
                                   n, _lib.stream_of(dev))
         _lib.check(st, "mm_pair_scan")

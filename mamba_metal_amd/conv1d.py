@@ -45,7 +45,7 @@ def causal_conv1d(x, weight, bias=None, *, apply_silu=True, out=None, conv_state
         if conv_state_out is not None:
             conv_state_out.zero_()
         return out
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.mm_causal_conv1d_fwd(
             x.data_ptr(), w.data_ptr(), _lib.ptr(bias), out.data_ptr(), _lib.ptr(conv_state_out),
             batch, seqlen, dim, width, (_lib._i64a3)(*x.stride()), (_lib._i64a3)(*out.stride()),
@@ -71,7 +71,7 @@ def conv_step(conv_state, x, weight, bias=None, *, apply_silu=True, out=None):
         raise ValueError("bias must be a contiguous (dim,) tensor of the weight's dtype")
     if out is None:
         out = torch.empty((batch, dim), dtype=x.dtype, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.mm_decode_conv_step(
             conv_state.data_ptr(), x.data_ptr(), w.data_ptr(), _lib.ptr(bias), out.data_ptr(),
             batch, dim, width, x.stride(0), out.stride(0), ws,

@@ -34,7 +34,7 @@ def ssm_step(ssm_state, x, dt, A, B, C, *, D=None, z=None, dt_bias=None, dt_soft
             raise ValueError(f"{name} must have x's dtype and unit inner stride")
     if out is None:
         out = torch.empty((batch, dim), dtype=x.dtype, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.mm_decode_ssm_step(
             ssm_state.data_ptr(), x.data_ptr(), dt.data_ptr(), _lib.ptr(dt_bias), A.data_ptr(),
             B.data_ptr(), C.data_ptr(), _lib.ptr(D), _lib.ptr(z), out.data_ptr(),
@@ -88,7 +88,7 @@ def ssm_step_dtproj(ssm_state, x, dt_in, dt_weight, A, B, C, *, dt_bias=None, D=
             raise ValueError(f"{name} must have x's dtype and unit inner stride")
     if out is None:
         out = torch.empty((batch, dim), dtype=x.dtype, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.mm_decode_ssm_step_dtproj(
             ssm_state.data_ptr(), x.data_ptr(), dt_in.data_ptr(), dt_weight.data_ptr(),
             _lib.ptr(dt_bias), A.data_ptr(), B.data_ptr(), C.data_ptr(), _lib.ptr(D), _lib.ptr(z),

@@ -58,7 +58,7 @@ def _make_packed(w: torch.Tensor) -> torch.Tensor:
     code = _lib.dtype_code(w.dtype)
     nbytes = lib.mm_packed_linear_weight_bytes(N, K, code)
     packed = torch.empty(nbytes // w.element_size(), dtype=w.dtype, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.mm_pack_linear_weight(w.data_ptr(), packed.data_ptr(), N, K, w.stride(0), code,
                                        _lib.stream_of(dev))
     _lib.check(st, "mm_pack_linear_weight")
@@ -108,7 +108,7 @@ def _call(prm: _lib.LinearParams, dev) -> None:
     ws = _workspace(dev, lib.mm_decode_linear_workspace_size(prm.M, prm.N, prm.K))
     if ws is not None:
         prm.workspace, prm.workspace_bytes = ws.data_ptr(), ws.numel()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.mm_decode_linear(ctypes.byref(prm), _lib.stream_of(dev))
     _lib.check(st, "mm_decode_linear")
 
@@ -222,7 +222,7 @@ def decode_in_proj_conv_xproj(x, w, conv_state, conv_w, conv_b, w_x, x_norm=None
                                                                      w_x.shape[0]))
     if ws is not None:
         prm.workspace, prm.workspace_bytes = ws.data_ptr(), ws.numel()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.mm_decode_in_proj_xproj(ctypes.byref(prm), packed_weight(w_x).data_ptr(),
                                          w_x.shape[0], x_dbl.data_ptr(), x_dbl.stride(0),
                                          _lib.stream_of(dev))

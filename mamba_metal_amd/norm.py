@@ -23,7 +23,7 @@ def add_rmsnorm(resid, add, weight, eps, out=None):
     if out is None:
         out = torch.empty_like(resid)
     o2 = out.reshape(-1, dim)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.mm_add_rmsnorm(r2.data_ptr(), _lib.ptr(a2), weight.data_ptr(), o2.data_ptr(),
                                 r2.shape[0], dim, r2.stride(0), 0 if a2 is None else a2.stride(0),
                                 o2.stride(0), float(eps), _lib.dtype_code(resid.dtype),

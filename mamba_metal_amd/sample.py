@@ -23,7 +23,7 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
         out = torch.empty((rows,), dtype=torch.int64, device=dev)
     if out.shape != (rows,) or out.dtype != torch.int64 or not out.is_contiguous():
         raise ValueError("out must be a contiguous int64 (rows,) tensor")
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.mm_argmax_rows(logits.data_ptr(), rows, n, logits.stride(0),
                                 _lib.dtype_code(logits.dtype), out.data_ptr(), _lib.stream_of(dev))
     _lib.check(st, "mm_argmax_rows")

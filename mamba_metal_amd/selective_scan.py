@@ -133,7 +133,7 @@ def selective_scan_into(u, delta, A, B, C, y, *, D=None, z=None, delta_softplus=
     p.delta_softplus = 1 if delta_softplus else 0
     p.reserved = 0
     p.status = _status_word(dev).data_ptr()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.mm_selective_scan_fwd_strided(p, _lib.stream_of(dev))
     _lib.check(st, "mm_selective_scan_fwd_strided")
     return y
