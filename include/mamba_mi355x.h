@@ -145,9 +145,11 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* p, void* stream);
  * serving loops, harnesses that forbid hipMalloc).  Same arguments, semantics and
  * results as mm_selective_scan_fwd, without the workspace: the library keeps one scan
  * workspace of MM_SCAN_SCRATCH_BYTES per device in a static device array, held until
- * the process ends.  Shapes whose mm_selective_scan_workspace_size exceeds
- * MM_SCAN_SCRATCH_BYTES are rejected with MM_ERR_WORKSPACE (host-side, before any HIP
- * call).  It calls no allocating routine.  Every call on a device uses that device's
+ * the process ends.  When mm_selective_scan_workspace_size exceeds
+ * MM_SCAN_SCRATCH_BYTES only because of the split scan's segment summaries, the call runs
+ * the chained scan (the same result up to fp32 rounding); shapes whose chained share
+ * exceeds it too are rejected with MM_ERR_WORKSPACE (host-side, before any HIP call).
+ * It calls no allocating routine.  Every call on a device uses that device's
  * array, so calls that overlap in time on one device race (order them on one stream);
  * the array's status word is not visible to the caller. */
 #define MM_SCAN_SCRATCH_BYTES (32u << 20)

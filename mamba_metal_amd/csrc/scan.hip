@@ -912,21 +912,14 @@ int validate(const mm_scan_params* a) {
 }  // namespace scan
 }  // namespace mm
 
-extern "C" {
+namespace mm {
+namespace scan {
 
-size_t mm_selective_scan_workspace_size(int64_t batch, int64_t dim, int64_t dstate,
-                                        int64_t seqlen) {
-  using namespace mm::scan;
-  if (batch <= 0 || dim <= 0 || dstate < 1 || dstate > MM_MAX_DSTATE || seqlen < 0) return 0;
-  int groups = 8, spl = 2;
-  pick_shape(dstate, &groups, &spl);
-  return ws_layout(batch, dim, groups, spl, std::max<int64_t>(seqlen, 1)).total;
-}
-
-int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
-  using namespace mm;
-  using namespace mm::scan;
-  clear_error();
+// The scan behind both entry points.  The workspace must hold the layout's total;
+// with chained_min_ok (the allocation-free entry point, whose workspace is fixed) a
+// workspace that holds everything but the split scan's segment summaries also runs, on
+// the chained path.
+int fwd(const mm_scan_params* a, void* stream, bool chained_min_ok) {
   int st = validate(a);
   if (st != MM_OK) return st;
   if (a->batch == 0 || a->dim == 0) return MM_OK;
@@ -939,8 +932,9 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
   int layout = kTimeContig, vec_ok = 0;
   choose_layout(a, ept, &layout, &vec_ok);
   const WsLayout w = ws_layout(a->batch, a->dim, groups, spl, std::max<int64_t>(a->seqlen, 1));
-  if (a->workspace == nullptr || a->workspace_bytes < w.total)
-    return fail(MM_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu (%s)", w.total,
+  const size_t need = chained_min_ok ? w.sum : w.total;
+  if (a->workspace == nullptr || a->workspace_bytes < need)
+    return fail(MM_ERR_WORKSPACE, "workspace of %zu bytes required, got %zu (%s)", need,
                 a->workspace_bytes, a->workspace ? "too small" : "NULL");
   if (!aligned(a->workspace, 256)) return fail(MM_ERR_WORKSPACE, "workspace must be 256-byte aligned");
 
@@ -985,12 +979,12 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
   return check_launch("selective_scan");
 }
 
-int mm_selective_scan_fwd(const void* u, const void* delta, const float* A, const void* B,
-                          const void* C, const float* D, const void* z, void* y,
-                          float* ssm_state_out, int64_t batch, int64_t dim, int64_t dstate,
-                          int64_t seqlen, int32_t x_dtype, int32_t bc_dtype,
-                          int32_t delta_softplus, void* workspace, size_t workspace_bytes,
-                          void* stream) {
+// mm_scan_params of the reference-shaped (row-major contiguous) entry points.
+mm_scan_params contiguous_params(const void* u, const void* delta, const float* A, const void* B,
+                                 const void* C, const float* D, const void* z, void* y,
+                                 float* ssm_state_out, int64_t batch, int64_t dim, int64_t dstate,
+                                 int64_t seqlen, int32_t x_dtype, int32_t bc_dtype,
+                                 int32_t delta_softplus) {
   mm_scan_params a = {};
   a.u = u;
   a.delta = delta;
@@ -1001,8 +995,6 @@ int mm_selective_scan_fwd(const void* u, const void* delta, const float* A, cons
   a.z = z;
   a.y = y;
   a.state_out = ssm_state_out;
-  a.workspace = workspace;
-  a.workspace_bytes = workspace_bytes;
   a.batch = batch;
   a.dim = dim;
   a.dstate = dstate;
@@ -1019,6 +1011,39 @@ int mm_selective_scan_fwd(const void* u, const void* delta, const float* A, cons
   a.x_dtype = x_dtype;
   a.bc_dtype = bc_dtype;
   a.delta_softplus = delta_softplus;
+  return a;
+}
+
+}  // namespace scan
+}  // namespace mm
+
+extern "C" {
+
+size_t mm_selective_scan_workspace_size(int64_t batch, int64_t dim, int64_t dstate,
+                                        int64_t seqlen) {
+  using namespace mm::scan;
+  if (batch <= 0 || dim <= 0 || dstate < 1 || dstate > MM_MAX_DSTATE || seqlen < 0) return 0;
+  int groups = 8, spl = 2;
+  pick_shape(dstate, &groups, &spl);
+  return ws_layout(batch, dim, groups, spl, std::max<int64_t>(seqlen, 1)).total;
+}
+
+int mm_selective_scan_fwd_strided(const mm_scan_params* a, void* stream) {
+  mm::clear_error();
+  return mm::scan::fwd(a, stream, false);
+}
+
+int mm_selective_scan_fwd(const void* u, const void* delta, const float* A, const void* B,
+                          const void* C, const float* D, const void* z, void* y,
+                          float* ssm_state_out, int64_t batch, int64_t dim, int64_t dstate,
+                          int64_t seqlen, int32_t x_dtype, int32_t bc_dtype,
+                          int32_t delta_softplus, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  mm_scan_params a = mm::scan::contiguous_params(u, delta, A, B, C, D, z, y, ssm_state_out, batch,
+                                                 dim, dstate, seqlen, x_dtype, bc_dtype,
+                                                 delta_softplus);
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
   return mm_selective_scan_fwd_strided(&a, stream);
 }
 
@@ -1070,28 +1095,18 @@ extern "C" int mm_selective_scan_fwd_noalloc(const void* u, const void* delta, c
                                              int32_t delta_softplus, void* stream) {
   using namespace mm;
   clear_error();
-  mm_scan_params a = {};
-  a.u = u;
-  a.delta = delta;
-  a.A = A;
-  a.B = B;
-  a.C = C;
-  a.D = D;
-  a.z = z;
-  a.y = y;
-  a.state_out = ssm_state_out;
-  a.batch = batch;
-  a.dim = dim;
-  a.dstate = dstate;
-  a.seqlen = seqlen;
-  a.x_dtype = x_dtype;
-  a.bc_dtype = bc_dtype;
-  a.delta_softplus = delta_softplus;
+  mm_scan_params a = scan::contiguous_params(u, delta, A, B, C, D, z, y, ssm_state_out, batch, dim,
+                                             dstate, seqlen, x_dtype, bc_dtype, delta_softplus);
   // host-only checks first (no HIP call before the arguments are known to be valid)
   int st = scan::validate(&a);
   if (st != MM_OK) return st;
   if (batch == 0 || dim == 0) return MM_OK;
-  const size_t need = mm_selective_scan_workspace_size(batch, dim, dstate, seqlen);
+  // The fixed array must hold at least the chained scan's share of the workspace; the
+  // split scan's segment summaries are used only when they fit too.
+  int groups = 8, spl = 2;
+  scan::pick_shape(dstate, &groups, &spl);
+  const size_t need =
+      scan::ws_layout(batch, dim, groups, spl, std::max<int64_t>(seqlen, 1)).sum;
   if (need > MM_SCAN_SCRATCH_BYTES)
     return fail(MM_ERR_WORKSPACE,
                 "batch=%lld dim=%lld dstate=%lld seqlen=%lld needs %zu bytes of scan workspace; "
@@ -1102,7 +1117,7 @@ extern "C" int mm_selective_scan_fwd_noalloc(const void* u, const void* delta, c
   void* ptr = nullptr;
   st = scratch_address(&ptr);
   if (st != MM_OK) return st;
-  return mm_selective_scan_fwd(u, delta, A, B, C, D, z, y, ssm_state_out, batch, dim, dstate,
-                               seqlen, x_dtype, bc_dtype, delta_softplus, ptr,
-                               MM_SCAN_SCRATCH_BYTES, stream);
+  a.workspace = ptr;
+  a.workspace_bytes = MM_SCAN_SCRATCH_BYTES;
+  return scan::fwd(&a, stream, true);
 }

@@ -3,7 +3,8 @@
 Its output must equal mm_selective_scan_fwd's (same kernels; the workspace is the
 library's static per-device array instead of a caller-allocated buffer), on two calls
 in a row -- the second smaller than the first, so the array holds the first call's
-contents when the second starts -- plus a shape beyond the array, which is rejected.
+contents when the second starts; a shape whose split-scan summaries do not fit the array
+runs chained; a shape beyond the array is rejected.
 """
 
 from __future__ import annotations
@@ -68,6 +69,31 @@ def test_noalloc_matches_workspace_entry_point(dev):
         assert torch.isfinite(y0).all() and torch.isfinite(h0).all()
         assert torch.equal(y1, y0), f"{shape}: y differs"
         assert torch.equal(h1, h0), f"{shape}: state differs"
+
+
+def test_noalloc_chained_when_summaries_do_not_fit(dev):
+    """B=4, D=4096 (256 64-channel blocks), L=32768: the full workspace (with the split
+    scan's segment summaries) exceeds the static array, the chained share fits, so the
+    allocation-free call runs the chained scan while the caller-allocated one splits.
+    The two paths round differently (a segment's carried decay is a product of exp2s in
+    one, exp2 of a sum in the other): equal at the fp16 bar, on every output."""
+    from mamba_metal_amd import _lib
+
+    from helpers import assert_close
+
+    lib = _lib.load()
+    shape = (4, 4096, 32768)
+    need = lib.mm_selective_scan_workspace_size(shape[0], shape[1], 16, shape[2])
+    assert need > _lib.SCAN_SCRATCH_BYTES
+    ins = _inputs(dev, *shape, 4)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    y0, h0 = _call(lib, "fwd", ins, ws)
+    y1, h1 = _call(lib, "noalloc", ins)
+    torch.cuda.synchronize()
+    assert int(ws[4:8].view(torch.int32).item()) == 0
+    assert torch.isfinite(y1).all() and torch.isfinite(h1).all()
+    assert_close(y1.float().cpu().numpy(), y0.float().cpu().numpy(), 1e-3, 1e-3, "y")
+    assert_close(h1.cpu().numpy(), h0.cpu().numpy(), 1e-3, 1e-3, "state")
 
 
 def test_noalloc_rejects_oversize(dev):
