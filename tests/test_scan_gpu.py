@@ -390,6 +390,15 @@ def test_split_long_sequence_160_blocks(oracle_lib, dev):
     _blockwise_parity(oracle_lib, dev, 2, 5120, 32768, seed=6)
 
 
+@pytest.mark.parametrize("dim,seqlen", [(16352, 512), (16384, 512), (32736, 256), (32768, 256)])
+def test_grid_regime_boundaries(oracle_lib, dev, dim, seqlen):
+    """Chain counts (32-channel blocks, batch 1) on either side of the persistent grid's
+    switches on a 256-CU part: 511 / 512 chains (all resident slots / two workgroups per
+    CU) and 1023 / 1024 (two per CU / all slots).  One channel of every block against the
+    oracle."""
+    _blockwise_parity(oracle_lib, dev, 1, dim, seqlen, seed=dim % 97)
+
+
 def test_config2_full_size_every_block(oracle_lib, dev):
     _blockwise_parity(oracle_lib, dev, 8, 1536, 8192, seed=2)
 
