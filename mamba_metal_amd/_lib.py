@@ -196,16 +196,28 @@ def on_device(device: torch.device):
     return torch.cuda.device(device)
 
 
+_DEVICES: dict = {}  # device index -> torch.device (one object per index)
+
+
 def require_cuda(*tensors) -> torch.device:
-    dev = None
+    """The one GPU all given tensors (None entries skipped) live on; raises otherwise.
+    Device indices are compared as ints: called a few times per layer of a model prefill,
+    where building a torch.device per tensor showed up in the host time."""
+    idx = None
     for t in tensors:
         if t is None:
             continue
-        if not t.is_cuda:
+        i = t.get_device()
+        if i < 0 or not t.is_cuda:
             raise ValueError("mamba_metal_amd ops need GPU (HIP) tensors; got a tensor on "
                              f"{t.device} (there is no CPU fallback)")
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+        if idx is None:
+            idx = i
+        elif i != idx:
+            raise ValueError(f"tensors on different devices: cuda:{idx} and cuda:{i}")
+    if idx is None:
+        return None
+    dev = _DEVICES.get(idx)
+    if dev is None:
+        dev = _DEVICES.setdefault(idx, torch.device("cuda", idx))
     return dev

@@ -41,6 +41,7 @@ def _common_dtype(*ts):
 
 
 _STATUS: dict = {}   # device -> persistent int32 status word every scan ORs into
+_WS_BYTES: dict = {}  # (batch, dim, dstate, seqlen) -> workspace bytes (a pure function)
 
 
 def _dev_of(device) -> torch.device:
@@ -108,7 +109,10 @@ def selective_scan_into(u, delta, A, B, C, y, *, D=None, z=None, delta_softplus=
         assert state_out.shape == (batch, dim, dstate) and state_out.is_contiguous()
         assert state_out.dtype == torch.float32
 
-    ws_bytes = lib.mm_selective_scan_workspace_size(batch, dim, dstate, seqlen)
+    key = (batch, dim, dstate, seqlen)
+    ws_bytes = _WS_BYTES.get(key)
+    if ws_bytes is None:
+        ws_bytes = _WS_BYTES.setdefault(key, lib.mm_selective_scan_workspace_size(*key))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
 
     p = _lib.ScanParams()
