@@ -118,7 +118,7 @@ struct WsLayout {
 
 // The split pays for at most kSplitMaxChains 64-channel blocks, and up to twice that for
 // long sequences (>= kSplitLongTiles tiles), where a chain's walk dominates: measured at
-// B=2 D=5120 (160 blocks) L=32768 2.33 -> 2.14 ms, but at L=8192 (B=8 D=1536, 192 blocks)
+// B=2 D=5120 (160 blocks) L=32768 2.34 -> 2.20 ms, but at L=8192 (B=8 D=1536, 192 blocks)
 // 0.65 -> 0.79 ms and at L=4096 (B=3 D=5120, 240 blocks) 0.36 -> 0.43 ms, where the second
 // pass over the inputs costs more than the chain walk it shortens.
 constexpr int64_t kSplitLongTiles = 512;
