@@ -322,8 +322,8 @@ __global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_dtproj_kernel(const
       dot = __builtin_fmaf(d.z, w[4 * i + 2], dot);
       dot = __builtin_fmaf(d.w, w[4 * i + 3], dot);
     }
-    dot += __shfl_xor(dot, 1, 64);
-    dot += __shfl_xor(dot, 2, 64);
+    dot += lane_xor(dot, 1);
+    dot += lane_xor(dot, 2);
     const float xv = Ty<DT>::f(xr[bb]);
     const float dtv = softplus_full(dot + bias);
     const float du = dtv * xv;
@@ -336,8 +336,8 @@ __global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_dtproj_kernel(const
       acc = __builtin_fmaf(hs[k], s_C[bb][q * 4 + k], acc);
     }
     if (cok) *reinterpret_cast<float4*>(hw + bb * p.dim * kFusedNS) = make_float4(hs[0], hs[1], hs[2], hs[3]);
-    acc += __shfl_xor(acc, 1, 64);
-    acc += __shfl_xor(acc, 2, 64);
+    acc += lane_xor(acc, 1);
+    acc += lane_xor(acc, 2);
     if (q == 0 && cok) {
       acc = __builtin_fmaf(Dr, xv, acc);
       if (p.z) acc *= silu_f(Ty<DT>::f(zr[bb]));
@@ -475,8 +475,8 @@ __global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_mfma_kernel(const F
       yacc = __builtin_fmaf(hs[k], s_C[bb][q * 4 + k], yacc);
     }
     if (cok) *reinterpret_cast<float4*>(hw + bb * p.dim * kFusedNS) = make_float4(hs[0], hs[1], hs[2], hs[3]);
-    yacc += __shfl_xor(yacc, 1, 64);
-    yacc += __shfl_xor(yacc, 2, 64);
+    yacc += lane_xor(yacc, 1);
+    yacc += lane_xor(yacc, 2);
     if (q == 0 && cok) {
       yacc = __builtin_fmaf(Dr, xv, yacc);
       if (p.z) yacc *= silu_f(Ty<DT>::f(zr[bb]));

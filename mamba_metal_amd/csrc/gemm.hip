@@ -278,7 +278,7 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
       const T* const r = static_cast<const T*>(p.x) + m * p.ldx;
       float ss = row_sumsq<DT>(r, nch, lane);
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      for (int off = 32; off > 0; off >>= 1) ss += lane_xor(ss, off);
       const float inv = rsqrtf(ss / static_cast<float>(p.K) + p.x_eps);
       if ((lane >> 3) == m) xinv = inv;
     }
@@ -832,7 +832,7 @@ __global__ __launch_bounds__(256) void reduce_norm_kernel(const LinParams p) {
     if (ok) rrow[tid + 256 * u] = o;
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  for (int off = 32; off > 0; off >>= 1) ss += lane_xor(ss, off);
   if ((tid & 63) == 0) s_part[tid >> 6] = ss;
   __syncthreads();
   const float inv = rsqrtf((s_part[0] + s_part[1] + s_part[2] + s_part[3]) / static_cast<float>(p.N) + p.eps);
@@ -911,7 +911,7 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
         const T* const r = static_cast<const T*>(p.x) + m * p.ldx;
         float ss = row_sumsq<DT>(r, nch, lane);
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        for (int off = 32; off > 0; off >>= 1) ss += lane_xor(ss, off);
         if (lane == 0) s_inv[m] = rsqrtf(ss / static_cast<float>(p.K) + p.x_eps);
       }
     }
@@ -950,7 +950,7 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
 #pragma unroll
   for (int m = 0; m < MM; ++m) {
 #pragma unroll
-    for (int off = 8; off < 64; off <<= 1) acc[m] += __shfl_xor(acc[m], off, 64);
+    for (int off = 8; off < 64; off <<= 1) acc[m] += lane_xor(acc[m], off);
     if (lane < kGvCols) s_red[wave][m][lane] = acc[m];
   }
   __syncthreads();

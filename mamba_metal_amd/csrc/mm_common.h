@@ -161,6 +161,34 @@ __device__ __forceinline__ typename Ty<DT>::T norm_round(float x, float inv, flo
 // silu(z) = z * sigmoid(z) (selective_scan_chunked.metal:143).
 __device__ __forceinline__ float silu_f(float z) { return z * rcp_hw(1.0f + exp2_hw(-z * kLog2e)); }
 
+// v of lane (lane ^ m) within the wave, for m = 1, 2, 4, 8, 16, 32, on VALU cross-lane
+// operations instead of an LDS permute (ds_bpermute, a ~100-cycle round trip on the
+// reductions' critical path): DPP quad permutes for 1 and 2, the half-row mirror
+// (lane ^ 7) then a quad reverse (^ 3) for 4, a 16-lane row rotation by 8 for 8, and
+// gfx950's v_permlane16 / v_permlane32 swaps (which hand both halves to every lane) for
+// 16 and 32.  The whole wave must be active, as at every call site.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_xor(float v, int m) {
+  switch (m) {
+    case 1: return dpp_mov<0xB1>(v);                    // quad_perm [1,0,3,2]
+    case 2: return dpp_mov<0x4E>(v);                    // quad_perm [2,3,0,1]
+    case 4: return dpp_mov<0x1B>(dpp_mov<0x141>(v));    // half-row mirror, quad_perm [3,2,1,0]
+    case 8: return dpp_mov<0x128>(v);                   // row_ror:8
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+      return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+    }
+    case 32: {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+      return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+    }
+    default: return __shfl_xor(v, m, 64);
+  }
+}
+
 // softplus with the reference's cutoff: x <= 20 ? log(1 + exp(x)) : x
 // (selective_scan_chunked.metal:60-65).  log1p is evaluated as
 // log(s) * e / (s - 1) with s = 1 + e (Goldberg's log1p correction) so tiny e

@@ -70,7 +70,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_vec_kernel(
     }
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  for (int off = 32; off > 0; off >>= 1) ss += lane_xor(ss, off);
   const float inv = rsqrtf(ss / static_cast<float>(dim) + eps);
   T* o = static_cast<T*>(out) + row * out_stride;
 #pragma unroll
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(
   }
   // wave reduction, then across the 4 waves
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  for (int off = 32; off > 0; off >>= 1) ss += lane_xor(ss, off);
   if ((tid & 63) == 0) s_part[tid >> 6] = ss;
   __syncthreads();
   float tot = 0.0f;
