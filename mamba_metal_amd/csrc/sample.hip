@@ -76,34 +76,29 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const void* __restrict
   }
   // Across threads: full comparison (value, then index); a thread with no element
   // carries index n, which loses to every real element.
-  int64_t bl = bi < 0 ? n : bi;
+  // Indices fit int32 (n <= 2^30, checked on the host) and move between lanes as raw bits.
+  int32_t bl = bi < 0 ? n32 : bi;
   if (bi < 0) bv = -__builtin_inff();
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float ov = __shfl_xor(bv, off, 64);
-    const int64_t oi = __shfl_xor(bl, off, 64);
-    if (better(ov, oi, bv, bl)) {
-      bv = ov;
-      bl = oi;
+  auto xchg = [](float& v, int32_t& i, int off) __attribute__((always_inline)) {
+    const float ov = lane_xor(v, off);
+    const int32_t oi = __float_as_int(lane_xor(__int_as_float(i), off));
+    if (better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
     }
-  }
+  };
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) xchg(bv, bl, off);
   if ((tid & 63) == 0) {
     s_v[tid >> 6] = bv;
-    s_i[tid >> 6] = static_cast<int32_t>(bl);
+    s_i[tid >> 6] = bl;
   }
   __syncthreads();
-  if (tid < 64) {
+  if (tid < 64) {  // all of wave 0
     bv = tid < kThreads / 64 ? s_v[tid] : -__builtin_inff();
-    bl = tid < kThreads / 64 ? s_i[tid] : n;
+    bl = tid < kThreads / 64 ? s_i[tid] : n32;
 #pragma unroll
-    for (int off = 8; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int64_t oi = __shfl_xor(bl, off, 64);
-      if (better(ov, oi, bv, bl)) {
-        bv = ov;
-        bl = oi;
-      }
-    }
+    for (int off = 8; off > 0; off >>= 1) xchg(bv, bl, off);
     if (tid == 0) out[blockIdx.x] = bl;
   }
 }
