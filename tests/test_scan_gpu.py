@@ -269,8 +269,8 @@ def test_config0_against_golden(dev):
     assert_close(h, g["state"], 1e-5, 1e-5, "config0 state")
 
 
-def _blockwise_parity(oracle_lib, dev, batch, dim, seqlen, seed):
-    """Full-size fp16 scan on the GPU; the fp64 oracle on one channel of EVERY 32-channel
+def _blockwise_parity(oracle_lib, dev, batch, dim, seqlen, seed, dtype=torch.float16):
+    """Full-size fp16 (or bf16) scan on the GPU; the fp64 oracle on one channel of EVERY 32-channel
     block (a random lane per block, plus the first and last channel): the kernel's
     chains are blocks of 64 or 32 channels, each with its own segment hand-offs, so every
     chain's hand-offs are checked.  Channels are independent, so a subset must match the
@@ -280,7 +280,7 @@ def _blockwise_parity(oracle_lib, dev, batch, dim, seqlen, seed):
 
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
-    f16 = torch.float16
+    f16 = dtype
     u = torch.randn((batch, dim, seqlen), generator=g, device=dev, dtype=torch.float32).to(f16)
     d = (torch.randn((batch, dim, seqlen), generator=g, device=dev) * 0.5 - 1.0).to(f16)
     z = torch.randn((batch, dim, seqlen), generator=g, device=dev).to(f16)
@@ -306,7 +306,8 @@ def _blockwise_parity(oracle_lib, dev, batch, dim, seqlen, seed):
                                            C[b:b + 1].float().cpu().numpy(),
                                            D=D.index_select(0, idx).cpu().numpy(), z=pick(z),
                                            delta_softplus=True)
-        assert_close(pick(y), yo, 1e-3, 1e-3, f"batch {b} channels {chans.tolist()} y")
+        ytol = 1e-3 if dtype == torch.float16 else 8e-3  # bf16 output rounding
+        assert_close(pick(y), yo, ytol, ytol, f"batch {b} channels {chans.tolist()} y")
         assert_close(h[b:b + 1].index_select(1, idx).cpu().numpy(), ho, 1e-3, 1e-3,
                      f"batch {b} state")
         checked += len(chans)
@@ -397,6 +398,12 @@ def test_grid_regime_boundaries(oracle_lib, dev, dim, seqlen):
     CU) and 1023 / 1024 (two per CU / all slots).  One channel of every block against the
     oracle."""
     _blockwise_parity(oracle_lib, dev, 1, dim, seqlen, seed=dim % 97)
+
+
+def test_bf16_large_every_block(oracle_lib, dev):
+    """bf16 inputs and output at B=2 D=5120 L=8192 (320 32-channel chains, the two
+    workgroups per CU grid): one channel of every block against the oracle."""
+    _blockwise_parity(oracle_lib, dev, 2, 5120, 8192, seed=7, dtype=torch.bfloat16)
 
 
 def test_config2_full_size_every_block(oracle_lib, dev):
