@@ -529,7 +529,8 @@ __global__ __launch_bounds__(64 * G, MM_SCAN_MIN_WG) void scan_kernel(
       Grp cur, nxt;
       constexpr bool kPipe = SPL <= 4;
       if (kPipe) fetch(0, nxt);
-#pragma unroll(kPipe ? 8 : 1)
+      constexpr int kGroupUnroll = kPipe ? 8 : 1;
+#pragma unroll kGroupUnroll
       for (int tt = 0; tt < kT; tt += 4) {
         if (kPipe) {
           cur = nxt;
