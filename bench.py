@@ -286,8 +286,10 @@ def cpu_decode_extras():
 
 
 def cpu_baseline(batch, dim, dstate, seqlen, n_channels=5120):
-    """C oracle (fp32 math, OpenMP) on n_channels of the workload -- a quarter of
-    config 4, about 12 s of CPU work on 16 threads -- scaled to all B*D."""
+    """C oracle (fp32 math, OpenMP over channels) on n_channels of the workload -- a
+    quarter of config 4: about 1 s of wall time on the GPU box's 16 host threads, i.e.
+    ~15 thread-seconds of CPU work -- scaled to all B*D.  This is config 4's all-threads
+    figure (``scan_configs`` adds its one-core figure)."""
     import numpy as np
 
     from oracle import cscan

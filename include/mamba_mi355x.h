@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 3
+#define MM_ABI_VERSION 4
 /* Largest d_state accepted: mamba_metal/selective_scan.py:9 (MAX_DSTATE = 64). */
 #define MM_MAX_DSTATE 64
 
@@ -126,7 +126,12 @@ typedef struct mm_scan_params {
   int32_t x_dtype;          /* mm_dtype of u, delta, z, y                        */
   int32_t bc_dtype;         /* mm_dtype of B, C                                  */
   int32_t delta_softplus;   /* nonzero: apply softplus to delta                  */
-  int32_t reserved;         /* must be 0                                         */
+  int32_t handoff_timeout_us; /* bound (microseconds) of a time segment's wait for its
+                               predecessor's carried state; 0 = the default, 2 s.  The
+                               wait always ends well before (a segment is claimed only
+                               after its predecessor); the bound keeps every wave's exit
+                               finite.  A wait that expires sets the status bits below
+                               and the call's y is not valid.                      */
   int32_t* status;          /* optional device int32 (NULL = none): the kernel ORs
                                MM_SCAN_STATUS_* bits into it when y is not valid.
                                The library never clears it, so one word can collect
@@ -150,14 +155,18 @@ int mm_selective_scan_fwd_strided(const mm_scan_params* p, void* stream);
  * the chained scan (the same result up to fp32 rounding); shapes whose chained share
  * exceeds it too are rejected with MM_ERR_WORKSPACE (host-side, before any HIP call).
  * It calls no allocating routine.  Every call on a device uses that device's
- * array, so calls that overlap in time on one device race (order them on one stream);
- * the array's status word is not visible to the caller. */
+ * array, so calls that overlap in time on one device race (order them on one stream).
+ * `status` is optional (NULL = none), a device int32 as mm_scan_params.status: the call
+ * ORs MM_SCAN_STATUS_* bits into it when its y is not valid; never cleared by the
+ * library.  The array's device address is looked up on the first call on each device
+ * (hipGetSymbolAddress, which does not allocate). */
 #define MM_SCAN_SCRATCH_BYTES (32u << 20)
 int mm_selective_scan_fwd_noalloc(const void* u, const void* delta, const float* A,
                                   const void* B, const void* C, const float* D, const void* z,
                                   void* y, float* ssm_state_out, int64_t batch, int64_t dim,
                                   int64_t dstate, int64_t seqlen, int32_t x_dtype,
-                                  int32_t bc_dtype, int32_t delta_softplus, void* stream);
+                                  int32_t bc_dtype, int32_t delta_softplus, int32_t* status,
+                                  void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* (b) Causal depthwise conv1d over time, channels-last -- replaces

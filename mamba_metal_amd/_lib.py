@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library; see module d
 
 LIB_NAME = "libmamba_mi355x.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 3
+ABI_VERSION = 4
 MAX_DSTATE = 64
 
 # mm_dtype
@@ -56,8 +56,8 @@ class ScanParams(ctypes.Structure):
         ("u_stride", _i64a3), ("delta_stride", _i64a3), ("z_stride", _i64a3),
         ("y_stride", _i64a3), ("B_stride", _i64a3), ("C_stride", _i64a3),
         ("A_stride", _i64a2), ("D_stride", _i64),
-        ("x_dtype", _i32), ("bc_dtype", _i32), ("delta_softplus", _i32), ("reserved", _i32),
-        ("status", _vp),
+        ("x_dtype", _i32), ("bc_dtype", _i32), ("delta_softplus", _i32),
+        ("handoff_timeout_us", _i32), ("status", _vp),
     ]
 
 
@@ -87,7 +87,7 @@ _SIGNATURES = {
     "mm_selective_scan_fwd": (
         [_vp] * 9 + [_i64] * 4 + [_i32, _i32, _i32, _vp, _sz, _vp], ctypes.c_int),
     "mm_selective_scan_fwd_strided": ([ctypes.POINTER(ScanParams), _vp], ctypes.c_int),
-    "mm_selective_scan_fwd_noalloc": ([_vp] * 9 + [_i64] * 4 + [_i32, _i32, _i32, _vp],
+    "mm_selective_scan_fwd_noalloc": ([_vp] * 9 + [_i64] * 4 + [_i32, _i32, _i32, _vp, _vp],
                                       ctypes.c_int),
     "mm_causal_conv1d_fwd": (
         [_vp] * 5 + [_i64] * 4 + [_i64a3, _i64a3, _i64a2, _i32, _i32, _i32, _vp], ctypes.c_int),

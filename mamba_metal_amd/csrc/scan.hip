@@ -37,27 +37,17 @@
 namespace mm {
 namespace scan {
 
-#ifndef MM_SCAN_G16
-#define MM_SCAN_G16 8
-#endif
-#ifndef MM_SCAN_SPL16
-#define MM_SCAN_SPL16 2
-#endif
-
 // Channels per workgroup: 64 (lane = channel) or, for the chained scan at dstate <= 16,
 // 32 (each half-wave takes the 32 channels with its own states).  kCpwMin sizes what
 // depends on the count of channel blocks (flags, tickets), kCpwMax what depends on the
 // padded channel count.
 constexpr int kCpwMax = 64;
 constexpr int kCpwMin = 32;
-#ifndef MM_SCAN_KT
-#define MM_SCAN_KT 32
-#endif
-#ifndef MM_SCAN_MIN_WG
-#define MM_SCAN_MIN_WG 1
-#endif
+// dstate <= 16: 8 state groups of 2 states (dstate <= 8: of 1 state).
+constexpr int kGroups16 = 8;
+constexpr int kSpl16 = 2;
 
-constexpr int kT = MM_SCAN_KT;  // timesteps per tile
+constexpr int kT = 32;  // timesteps per tile
 constexpr int kTP = kT + 4;  // padded LDS row length (floats)
 // The sequence is padded to whole groups of four tiles (the tile loop is unrolled by
 // four, without guards); padded steps are identity steps (delta' = 0, B = C = 0).
@@ -66,7 +56,9 @@ constexpr int kTGroup = 4;
 inline int64_t padded_len(int64_t seqlen) {
   return round_up(seqlen > 1 ? seqlen : 1, kTGroup * kT);
 }
-constexpr int kSpinLimit = 1 << 26;
+// Default bound of a segment's wait for its predecessor's carried state (a wait that
+// always ends, see the file comment; the bound only keeps every wave's exit finite).
+constexpr int64_t kDefaultHandoffTimeoutUs = 2000000;
 
 enum Layout { kTimeContig = 0, kChanContig = 1 };
 
@@ -84,6 +76,7 @@ struct Params {
   int32_t softplus;
   int32_t vec_ok;
   int* status;  // optional persistent status word (MM_SCAN_STATUS_* bits are ORed in)
+  uint64_t spin_ticks;  // hand-off wait bound in wall-clock (s_memrealtime) ticks
 };
 
 // Scan modes.  kChained: a unit starts from its predecessor's carried state (waits for
@@ -148,8 +141,8 @@ inline void pick_shape(int64_t dstate, int* groups, int* spl) {
   // 8 waves x 2 states for dstate <= 16 (enough waves per CU to hide the exp and LDS
   // latency at one workgroup per CU); 4 waves x SPL above.
   if (dstate <= 16) {
-    *groups = MM_SCAN_G16;
-    *spl = dstate <= 8 ? (MM_SCAN_SPL16 > 1 ? MM_SCAN_SPL16 / 2 : 1) : MM_SCAN_SPL16;
+    *groups = kGroups16;
+    *spl = dstate <= 8 ? kSpl16 / 2 : kSpl16;
   } else {
     *groups = 4;
     *spl = dstate <= 32 ? 8 : 16;
@@ -229,7 +222,7 @@ __device__ __forceinline__ float softplus_log2(float x) {
 
 // ---------------------------------------------------------------------------
 template <int DT, int LAYOUT, int SPL, int G, bool VEC, int MODE, int CPW>
-__global__ __launch_bounds__(64 * G, MM_SCAN_MIN_WG) void scan_kernel(
+__global__ __launch_bounds__(64 * G, 1) void scan_kernel(
     const Params p, const void* __restrict__ u_, const void* __restrict__ delta_,
     const void* __restrict__ z_, void* __restrict__ y_, const float* __restrict__ bc_,
     float* __restrict__ state_out_, int* __restrict__ ctl_, float* __restrict__ carry_,
@@ -423,11 +416,15 @@ __global__ __launch_bounds__(64 * G, MM_SCAN_MIN_WG) void scan_kernel(
     }
     if (MODE == kChained && seg > 0) {
       if (tid == 0) {
-        int spins = 0;
+        // Bounded by wall-clock time (never expected to expire; it keeps every wave's
+        // exit finite).  Once one wait of this call has given up, y is invalid anyway
+        // and later waits return at once, so a failing call ends within one bound.
+        const uint64_t t_start = wall_clock64();
         while (__hip_atomic_load(&ctl_[64 + cb], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
                static_cast<int>(seg)) {
+          if (__hip_atomic_load(&ctl_[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
           __builtin_amdgcn_s_sleep(1);
-          if (++spins > kSpinLimit) {  // never expected; keeps every wave's exit bounded
+          if (wall_clock64() - t_start > p.spin_ticks) {
             __hip_atomic_store(&ctl_[1], MM_SCAN_STATUS_HANDOFF_TIMEOUT, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
             if (p.status != nullptr)
@@ -909,7 +906,8 @@ int validate(const mm_scan_params* a) {
     return fail(MM_ERR_DSTATE, "dstate=%lld outside [1, %d]", (long long)a->dstate, MM_MAX_DSTATE);
   if (!valid_dtype(a->x_dtype) || !valid_dtype(a->bc_dtype))
     return fail(MM_ERR_DTYPE, "bad dtype (x_dtype=%d bc_dtype=%d)", a->x_dtype, a->bc_dtype);
-  if (a->reserved != 0) return fail(MM_ERR_LAYOUT, "reserved field must be 0");
+  if (a->handoff_timeout_us < 0)
+    return fail(MM_ERR_SHAPE, "handoff_timeout_us=%d is negative", a->handoff_timeout_us);
   const int64_t ncb = max_blocks(a->batch, a->dim);
   if (ncb > (1LL << 30)) return fail(MM_ERR_SHAPE, "too many channel blocks (%lld)", (long long)ncb);
   return MM_OK;
@@ -967,6 +965,22 @@ int fwd(const mm_scan_params* a, void* stream, bool chained_min_ok) {
   p.softplus = a->delta_softplus ? 1 : 0;
   p.vec_ok = vec_ok;
   p.status = a->status;
+  {
+    // wall-clock counter rate (kHz) of this device, for the hand-off wait's time bound
+    static DeviceCache rate_cache;
+    const int64_t khz = device_cached(
+        rate_cache,
+        [] {
+          int dev = 0, r = 0;
+          if (hipGetDevice(&dev) != hipSuccess ||
+              hipDeviceGetAttribute(&r, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+            r = 0;
+          return r;
+        },
+        100000);
+    const int64_t us = a->handoff_timeout_us > 0 ? a->handoff_timeout_us : kDefaultHandoffTimeoutUs;
+    p.spin_ticks = static_cast<uint64_t>(us) * static_cast<uint64_t>(khz) / 1000u;
+  }
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t nctl = 64 + max_blocks(a->batch, a->dim);
@@ -1061,9 +1075,10 @@ int mm_selective_scan_fwd(const void* u, const void* delta, const float* A, cons
 // process ends.  In host code the array's name is only a stand-in for the symbol, so
 // its device address is taken once per device with hipGetSymbolAddress and kept in
 // scratch_ptr[device]; kernels are only ever given that address.  The launches are
-// those of mm_selective_scan_fwd (the B/C pack kernel clears the work-queue counter
-// and flags at the start of every call, so the previous call's contents do not
-// matter).  Calls that overlap in time on one GPU share the array and race.
+// those of mm_selective_scan_fwd (the B/C pack kernel clears the work-queue counter,
+// flags and status word at the start of every call, so the previous call's contents do
+// not matter; the caller's optional status word receives the call's outcome).  Calls
+// that overlap in time on one GPU share the array and race.
 namespace {
 
 static __device__ __align__(256) unsigned char scratch[MM_SCAN_SCRATCH_BYTES];
@@ -1098,11 +1113,13 @@ extern "C" int mm_selective_scan_fwd_noalloc(const void* u, const void* delta, c
                                              const void* z, void* y, float* ssm_state_out,
                                              int64_t batch, int64_t dim, int64_t dstate,
                                              int64_t seqlen, int32_t x_dtype, int32_t bc_dtype,
-                                             int32_t delta_softplus, void* stream) {
+                                             int32_t delta_softplus, int32_t* status,
+                                             void* stream) {
   using namespace mm;
   clear_error();
   mm_scan_params a = scan::contiguous_params(u, delta, A, B, C, D, z, y, ssm_state_out, batch, dim,
                                              dstate, seqlen, x_dtype, bc_dtype, delta_softplus);
+  a.status = status;
   // host-only checks first (no HIP call before the arguments are known to be valid)
   int st = scan::validate(&a);
   if (st != MM_OK) return st;

@@ -85,11 +85,14 @@ def reset_scan_status(device=None) -> None:
 
 
 def selective_scan_into(u, delta, A, B, C, y, *, D=None, z=None, delta_softplus=False,
-                        state_out=None):
+                        state_out=None, handoff_timeout_us: int = 0):
     """Run the scan writing into a caller-provided y (any strides, shape of u).
 
     ``state_out`` (batch, dim, dstate) contiguous float32 or None.  Used by the
-    model to pass its (batch, seqlen, dim) buffers as transposed views."""
+    model to pass its (batch, seqlen, dim) buffers as transposed views.
+    ``handoff_timeout_us`` bounds a time segment's wait for its predecessor's carried
+    state (0 = the library default, 2 s); a wait that expires sets the bit
+    ``_lib.SCAN_STATUS_HANDOFF_TIMEOUT`` of ``scan_status()`` and y is not valid."""
     lib = _lib.load()
     dev = _lib.require_cuda(u, delta, A, B, C, D, z, y, state_out)
     batch, dim, seqlen = u.shape
@@ -135,7 +138,7 @@ def selective_scan_into(u, delta, A, B, C, y, *, D=None, z=None, delta_softplus=
     p.x_dtype = _lib.dtype_code(xdt)
     p.bc_dtype = _lib.dtype_code(bcdt)
     p.delta_softplus = 1 if delta_softplus else 0
-    p.reserved = 0
+    p.handoff_timeout_us = int(handoff_timeout_us)
     p.status = _status_word(dev).data_ptr()
     with _lib.on_device(dev):
         st = lib.mm_selective_scan_fwd_strided(p, _lib.stream_of(dev))

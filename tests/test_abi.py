@@ -48,7 +48,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_version_and_status_names(lib):
-    assert lib.mm_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.mm_abi_version() == _lib.ABI_VERSION == 4
     assert lib.mm_status_name(0) == b"MM_OK"
     assert lib.mm_status_name(-3) == b"MM_ERR_DSTATE"
     assert lib.mm_status_name(-99) == b"MM_ERR_UNKNOWN"
@@ -151,8 +151,9 @@ def test_strided_null_params(lib):
     p.u = p.delta = p.A = p.B = p.C = p.y = FAKE
     p.batch, p.dim, p.dstate, p.seqlen = 1, 4, 4, 8
     p.workspace, p.workspace_bytes = FAKE, 1 << 20
-    p.reserved = 1
-    assert lib.mm_selective_scan_fwd_strided(ctypes.byref(p), None) == _lib.ERR_LAYOUT
+    p.handoff_timeout_us = -1
+    assert lib.mm_selective_scan_fwd_strided(ctypes.byref(p), None) == _lib.ERR_SHAPE
+    assert b"handoff_timeout_us" in lib.mm_last_error()
 
 
 def test_conv_and_decode_validation(lib):
@@ -295,12 +296,12 @@ def test_noalloc_scan_rejects_oversize_host_side(lib):
     batch, dim, seqlen = 8, 5120, 65536
     assert lib.mm_selective_scan_workspace_size(batch, dim, 16, seqlen) > _lib.SCAN_SCRATCH_BYTES
     st = lib.mm_selective_scan_fwd_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, None,
-                                           batch, dim, 16, seqlen, _lib.F16, _lib.F16, 1, None)
+                                           batch, dim, 16, seqlen, _lib.F16, _lib.F16, 1, None, None)
     assert st == _lib.ERR_WORKSPACE
     assert b"allocation-free" in lib.mm_last_error()
     assert lib.mm_selective_scan_fwd_noalloc(None, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, None,
-                                             1, 64, 16, 64, 1, 1, 1, None) == _lib.ERR_NULL_POINTER
+                                             1, 64, 16, 64, 1, 1, 1, None, None) == _lib.ERR_NULL_POINTER
     assert lib.mm_selective_scan_fwd_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, None,
-                                             1, 64, 65, 64, 1, 1, 1, None) == _lib.ERR_DSTATE
+                                             1, 64, 65, 64, 1, 1, 1, None, None) == _lib.ERR_DSTATE
     assert lib.mm_selective_scan_fwd_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, None,
-                                             0, 64, 16, 64, 1, 1, 1, None) == _lib.OK
+                                             0, 64, 16, 64, 1, 1, 1, None, None) == _lib.OK

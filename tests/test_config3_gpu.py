@@ -1,15 +1,17 @@
 """Config 3 (Mamba-2.8b shape, batch 64 decode, fp16) on the MI355X.
 
   * 2.8b width (d_model 2560, d_inner 5120, dt_rank 160, vocab 50280), batch 64,
-    2 layers: 64-token prompts, then 4 teacher-forced decode steps against the float64
+    2 layers: 64-token prompts, then 16 teacher-forced decode steps against the float64
     CPU oracle -- the decode kernels at the configuration's real shapes (the fused
     in_proj + conv + x_proj at 64 x 10240 x 2560, the MFMA SSM step at 64 x 5120, the
     split-K out_proj with the residual + RMSNorm reduce, the LM head), and the prefill
     scan's channel-contiguous path at 64 x 5120.
-  * the full 64-layer model at batch 64 through properties that hold at any size:
-    finite logits, prefill(L) then step == prefill(L + 1) at position L
-    (experiments/17-incremental/test_step.py:31-41), and the HIP-graph decode equal to
-    the eager decode, token for token.
+  * the full 64-layer model at batch 64 -- config 3's workload: 512-token prompts, then
+    256 greedy steps -- through properties that hold at any size: prefill(L) then step
+    == prefill(L + 1) at position L (experiments/17-incremental/test_step.py:31-41), with
+    the same argmax on every row whose top-2 margin exceeds twice the logit difference;
+    and the HIP-graph decode (what bench.py times) equal to the eager decode token for
+    token over all 256 steps, with finite logits at every eager step.
 """
 
 from __future__ import annotations
@@ -43,21 +45,22 @@ def test_config3_width_two_layers_against_oracle(dev):
                              cfg.expand, cfg.dt_rank, cfg.rms_norm_eps),
                    {k: v.detach().float().cpu() for k, v in model.state_dict().items()})
     rng = np.random.default_rng(41)
+    n = 16
     ids = rng.integers(0, cfg.vocab_size, (64, 64))
-    teacher = rng.integers(0, cfg.vocab_size, (64, 4))
+    teacher = rng.integers(0, cfg.vocab_size, (64, n))
     reset_scan_status(dev)
     with torch.inference_mode():
         lg, convs, ssms = model.prefill(torch.as_tensor(ids, device=dev), last_only=True)
         gl = [lg[:, -1].float()]
-        for s in range(3):
+        for s in range(n - 1):
             lg, convs, ssms = model.step(torch.as_tensor(teacher[:, s:s + 1], device=dev), convs,
                                          ssms, inplace=True)
             gl.append(lg[:, 0].float())
     assert scan_status(dev) == 0
-    _, ref_logits = ref.generate_fast_ids(ids, 4, teacher=teacher)
+    _, ref_logits = ref.generate_fast_ids(ids, n, teacher=teacher)
     got = np.stack([g.argmax(-1).cpu().numpy() for g in gl], 1)
     # the logits of 64 rows x 50280 tokens span about +-35 here: 3e-2 absolute is ~1e-3 of that
-    check_greedy(got, gl, ref_logits, 4, "config-3 width, 2 layers, batch 64", tol=3e-2)
+    check_greedy(got, gl, ref_logits, n, "config-3 width, 2 layers, batch 64", tol=3e-2)
 
 
 @pytest.fixture(scope="module")
@@ -83,18 +86,45 @@ def test_config3_full_depth_prefill_step_invariant(dev, full_c3):
     err = float((full - st).abs().max())
     scale = float(full.abs().max())
     agree = float((full.argmax(-1) == st.argmax(-1)).float().mean())
+    top2 = full.topk(2, dim=-1).values
+    margin = (top2[:, 0] - top2[:, 1]).cpu().numpy()
+    checked = margin > 2 * err
+    same = (full.argmax(-1) == st.argmax(-1)).cpu().numpy()
     print(f"[config3 64 layers] prefill(513) vs prefill(512)+step: max |d logit| {err:.3e}, "
-          f"max |logit| {scale:.3f}, argmax agreement {agree:.3f}")
-    assert err < 0.03 * scale
-    assert agree >= 0.9
+          f"max |logit| {scale:.3f}, argmax agreement {agree:.3f}, "
+          f"{int((~checked).sum())} of 64 rows margin-exempt (top-2 margin <= {2 * err:.2e})")
+    assert err < 0.01 * scale
+    assert same[checked].all(), f"argmax differs on rows {np.nonzero(checked & ~same)[0].tolist()}"
+    assert (~checked).sum() <= 0.1 * 64
 
 
 def test_config3_full_depth_graph_equals_eager(dev, full_c3):
-    from mamba_metal_amd import generate_fast_ids
+    """Config 3's decode workload at full depth: batch 64, 512-token prompts, 256 greedy
+    steps replayed from the captured HIP graph equal the eager steps token for token, and
+    every eager step's logits are finite."""
+    from mamba_metal_amd import GraphDecoder
+    from mamba_metal_amd.generate import _argmax
 
     model, cfg = full_c3
+    n = 256
     rng = np.random.default_rng(44)
-    ids = torch.as_tensor(rng.integers(0, cfg.vocab_size, (64, 128)), device=dev)
-    eager = generate_fast_ids(model, ids, 8)
-    graph = generate_fast_ids(model, ids, 8, use_graph=True)
-    assert torch.equal(eager, graph)
+    ids = torch.as_tensor(rng.integers(0, cfg.vocab_size, (64, 512)), device=dev)
+    with torch.inference_mode():
+        lg, convs, ssms = model.prefill(ids, last_only=True)
+        tok = _argmax(lg[:, -1])
+        eager, finite = [tok], torch.ones((), dtype=torch.bool, device=dev)
+        for _ in range(n - 1):
+            lg, convs, ssms = model.step(tok.view(-1, 1), convs, ssms, inplace=True)
+            finite &= torch.isfinite(lg).all()
+            tok = _argmax(lg[:, 0])
+            eager.append(tok)
+        eager = torch.stack(eager, 1)
+    assert bool(finite), "non-finite logits in the eager decode"
+    print(f"[config3 64 layers] eager decode: {n} steps done", flush=True)
+    dec = GraphDecoder(model, 64, use_graph=True)
+    graph = [dec.start(ids).clone()]
+    for _ in range(n - 1):
+        graph.append(dec.step().clone())
+    graph = torch.stack(graph, 1)
+    diff = (graph != eager).any(0).nonzero()
+    assert diff.numel() == 0, f"graph decode differs from eager from step {int(diff[0])} on"

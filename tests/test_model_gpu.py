@@ -288,31 +288,38 @@ def test_load_mamba_hf_roundtrip(dev, tmp_path):
         assert torch.equal(model(ids), m2(ids))
 
 
-def test_config1_long_prompt_teacher_forced(dev):
-    """Config 1's workload shape end to end: 130m width and depth, fp16, a 2048-token
-    prompt (the fp16 split-mode prefill scan: 24 channel chains), then 32 teacher-forced
-    decode steps against the float64 oracle (experiments/18-prefill/bench_prefill.py:20-26
-    checks greedy equality after parallel prefill at prompts of 71-5601 tokens)."""
+def test_config1_workload_greedy(dev):
+    """Config 1's whole workload: 130m width and depth, fp16, a 2048-token prompt (the fp16
+    split-mode prefill scan: 48 channel chains), then 128 free-running greedy decode steps.
+    Every one of the 128 greedy ids is checked against the float64 oracle run teacher-forced
+    on the GPU's own ids (check_greedy: the id must be the oracle's argmax wherever the
+    oracle's top-2 margin exceeds twice the run's logit error), and the HIP-graph decoder
+    (what bench.py times) must produce the same 128 ids as the eager steps
+    (experiments/17-incremental/test_step.py:31-41, 18-prefill/bench_prefill.py:20-26)."""
     from mamba_metal_amd import generate_fast_ids
     from mamba_metal_amd.selective_scan import reset_scan_status, scan_status
 
+    n = 128
     model, cfg = make_model(dev, dtype=torch.float16, seed=12, d_model=768, n_layer=24,
                             vocab_size=50280, dt_rank=48)
     ref = ref_of(model, cfg)
     rng = np.random.default_rng(12)
     ids = torch.as_tensor(rng.integers(0, cfg.vocab_size, (1, 2048)), device=dev)
     reset_scan_status(dev)
-    got = generate_fast_ids(model, ids, 32).cpu().numpy()
+    got = generate_fast_ids(model, ids, n).cpu().numpy()
+    graph = generate_fast_ids(model, ids, n, use_graph=True).cpu().numpy()
     assert scan_status(dev) == 0
-    _, ref_logits = ref.generate_fast_ids(ids.cpu().numpy(), 32, teacher=got)
+    assert np.array_equal(graph, got), "graph decode differs from eager decode"
     with torch.inference_mode():
         lg, convs, ssms = model.prefill(ids, last_only=True)
         gl = [lg[:, -1].float()]
-        for s in range(31):
+        for s in range(n - 1):
             lg, convs, ssms = model.step(torch.as_tensor(got[:, s:s + 1], device=dev), convs, ssms,
                                          inplace=True)
             gl.append(lg[:, 0].float())
-    check_greedy(got, gl, ref_logits, 32, "config 1, 2048-token prompt")
+    print(f"[config1] oracle: prefill 2048 + {n - 1} teacher-forced steps (float64, CPU)", flush=True)
+    _, ref_logits = ref.generate_fast_ids(ids.cpu().numpy(), n, teacher=got)
+    check_greedy(got, gl, ref_logits, n, f"config 1, 2048-token prompt, {n} greedy steps")
 
 
 @pytest.mark.parametrize("L", [300, 2100])
@@ -411,9 +418,9 @@ def test_temperature_sampling_properties(dev, small):
 def test_decode_cost_constant_in_position(dev):
     """O(1) per token (experiments/17-incremental/constant_time.py): the decode step's time
     does not grow with the tokens already processed -- 64 graph-replayed steps after a
-    16-token prompt and after a 4000-token prompt take the same time (within 30%)."""
-    import time
-
+    16-token prompt and after a 4000-token prompt take the same time.  Timed with HIP
+    events on the replay stream, the minimum of three runs per prompt; the bar (1.5x) is
+    loose on purpose: a step whose cost grew with the prefix would be ~250x slower here."""
     from mamba_metal_amd import GraphDecoder
 
     model, cfg = make_model(dev, dtype=torch.float16, seed=14, d_model=256, n_layer=4,
@@ -421,16 +428,17 @@ def test_decode_cost_constant_in_position(dev):
     rng = np.random.default_rng(14)
     dec = GraphDecoder(model, 1, use_graph=True)
     times = {}
-    for L in (16, 4000, 16, 4000):
+    for L in (16, 4000) * 3:
         dec.start(torch.as_tensor(rng.integers(0, cfg.vocab_size, (1, L)), device=dev))
         for _ in range(8):
             dec.step()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
         for _ in range(64):
             dec.step()
+        e1.record()
         torch.cuda.synchronize()
-        times.setdefault(L, []).append((time.perf_counter() - t0) / 64)
+        times.setdefault(L, []).append(e0.elapsed_time(e1) / 64)
     short, long_ = min(times[16]), min(times[4000])
-    print(f"[constant-time] ms/step after 16 tokens {short * 1e3:.4f}, after 4000 {long_ * 1e3:.4f}")
-    assert long_ < 1.3 * short
+    print(f"[constant-time] ms/step after 16 tokens {short:.4f}, after 4000 {long_:.4f}")
+    assert long_ < 1.5 * short

@@ -72,13 +72,14 @@ def gpu_scan(inp, dev, dtype=torch.float32, bc_dtype=None, softplus=False, use_D
 
 
 def oracle_scan(oracle_lib, inp, dtype=torch.float32, bc_dtype=None, softplus=False, use_D=True,
-                use_z=True):
+                use_z=True, precision="f64"):
     bc_dtype = bc_dtype or dtype
     r = {k: rounded(inp[k], dtype) for k in ("u", "delta", "z")}
     r.update({k: rounded(inp[k], bc_dtype) for k in ("B", "C")})
     return oracle_lib.selective_scan(r["u"], r["delta"], inp["A"], r["B"], r["C"],
                                      D=inp["D"] if use_D else None,
-                                     z=r["z"] if use_z else None, delta_softplus=softplus)
+                                     z=r["z"] if use_z else None, delta_softplus=softplus,
+                                     precision=precision)
 
 
 def check(oracle_lib, dev, inp, what, dtype=torch.float32, bc_dtype=None, softplus=False,
@@ -154,13 +155,20 @@ def test_dstate_many_chains(oracle_lib, dev, N):
     64-channel blocks, past the split mode's 128): 32-channel blocks with 1 or 2 states per
     lane for N <= 16, 64-channel blocks with 8 or 16 for larger N; 4160 = 130 x 32, and a
     300-step sequence ends inside a tile.  y is a sum of N terms C[n]*h[n] of magnitude ~2-4
-    that largely cancel, so its fp32 rounding grows with N: over these 2.5 M outputs the
-    worst N = 64 element was 6.1e-5 off at |y| = 0.86 (one element past the plain 1e-5 bar);
-    the absolute bar scales as 1e-5 * N / 8 above N = 8 (states keep the plain bar)."""
+    that largely cancel, so its fp32 rounding grows with N (over these 2.5 M outputs the
+    worst N = 64 element was 6.1e-5 off at |y| = 0.86).  The bar is therefore set by a
+    plain fp32 evaluation of the same recurrence (the C oracle in fp32, libm expf): y's
+    absolute bar is the larger of 1e-5 and twice the fp32 oracle's own worst error against
+    the fp64 one on these inputs, so the kernel must be no worse than that; the states keep
+    the plain 1e-5 bar."""
     inp = features_inputs(2, 4160, N, 300, seed=100 + N)
     yg, hg = gpu_scan(inp, dev, torch.float32, None, True, True, True)
     yo, ho = oracle_scan(oracle_lib, inp, torch.float32, None, True, True, True)
-    assert_close(yg, yo, 1e-5, 1e-5 * max(1.0, N / 8), f"N={N} many chains y")
+    y32, _ = oracle_scan(oracle_lib, inp, torch.float32, None, True, True, True, precision="f32")
+    e32 = float(np.abs(y32.astype(np.float64) - yo).max())
+    eg = float(np.abs(np.asarray(yg, np.float64) - yo).max())
+    print(f"[dstate {N}] max |y - fp64 oracle|: kernel {eg:.2e}, fp32 oracle {e32:.2e}")
+    assert_close(yg, yo, 1e-5, max(1e-5, 2 * e32), f"N={N} many chains y")
     assert_close(hg, ho, 1e-5, 1e-5, f"N={N} many chains state")
 
 
@@ -421,3 +429,47 @@ def test_edges_against_golden(dev):
         y, h = gpu_scan(inp, dev, torch.float32, softplus=True)
         assert_close(y, g[f"y{i}"], 1e-5, 1e-5, f"edge {i} y")
         assert_close(h, g[f"state{i}"], 1e-5, 1e-5, f"edge {i} state")
+
+
+def test_handoff_timeout_is_reported_and_bounded(dev):
+    """Failure handling of the chained scan's segment hand-off, forced from the host: with
+    a 1-microsecond bound (every real predecessor segment takes far longer) the waits give
+    up, the kernel still exits, and the status word carries the timeout bit; the same call
+    with the default bound then completes with a clear status and the oracle's result
+    (one channel of every block).  640 chains of 32 channels, several segments each."""
+    from mamba_metal_amd import _lib
+    from mamba_metal_amd.selective_scan import (reset_scan_status, scan_status,
+                                                selective_scan_into)
+
+    import time
+
+    batch, dim, seqlen = 4, 5120, 8192
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    f16 = torch.float16
+    u = torch.randn((batch, dim, seqlen), generator=g, device=dev).to(f16)
+    d = (torch.randn((batch, dim, seqlen), generator=g, device=dev) * 0.5 - 1.0).to(f16)
+    B = torch.randn((batch, 16, seqlen), generator=g, device=dev).to(f16)
+    C = torch.randn((batch, 16, seqlen), generator=g, device=dev).to(f16)
+    A = -torch.arange(1, 17, device=dev, dtype=torch.float32).expand(dim, 16).contiguous()
+    y = torch.empty_like(u)
+    reset_scan_status(dev)
+    t0 = time.perf_counter()
+    selective_scan_into(u, d, A, B, C, y, delta_softplus=True, handoff_timeout_us=1)
+    torch.cuda.synchronize()
+    waited = time.perf_counter() - t0
+    assert scan_status(dev) & _lib.SCAN_STATUS_HANDOFF_TIMEOUT, "forced timeout not reported"
+    assert waited < 5.0, f"a timed-out call took {waited:.1f} s"
+    reset_scan_status(dev)
+    selective_scan_into(u, d, A, B, C, y, delta_softplus=True)
+    torch.cuda.synchronize()
+    assert scan_status(dev) == 0
+    from oracle import cscan
+
+    rng = np.random.default_rng(5)
+    chans = np.minimum(np.arange(dim // 32) * 32 + rng.integers(0, 32, dim // 32), dim - 1)
+    b = 2
+    uu, dd = u[b, chans].float().cpu().numpy()[None], d[b, chans].float().cpu().numpy()[None]
+    yr, _ = cscan.selective_scan(uu, dd, A[chans].cpu().numpy(), B[b:b + 1].float().cpu().numpy(),
+                                 C[b:b + 1].float().cpu().numpy(), delta_softplus=True)
+    assert_close(y[b, chans].float().cpu().numpy()[None], yr, 1e-3, 1e-3, "after timeout")
