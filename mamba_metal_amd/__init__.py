@@ -7,7 +7,8 @@ include/mamba_mi355x.h); projections use torch GEMMs.  There is no CPU fallback.
 """
 
 from mamba_metal_amd._loader import load_kernel
-from mamba_metal_amd.generate import GraphDecoder, generate, generate_fast, generate_fast_ids
+from mamba_metal_amd.generate import (GraphDecoder, GraphPrefill, generate, generate_fast,
+                                      generate_fast_ids)
 from mamba_metal_amd.load_hf import load_mamba_hf
 from mamba_metal_amd.mamba_block import MambaBlock
 from mamba_metal_amd.mamba_model import MambaConfig, MambaModel, MambaResidualBlock, init_weights_
@@ -25,6 +26,7 @@ __all__ = [
     "selective_scan",
     # extensions beyond the reference's API
     "GraphDecoder",
+    "GraphPrefill",
     "generate_fast_ids",
     "init_weights_",
 ]

@@ -11,7 +11,11 @@ Token-level API for serving and benchmarks (no tokenizer, batch > 1, no EOS):
   generate_fast_ids  prefill + decode on token ids, greedy or sampled.
   GraphDecoder       the decode step (embedding -> layers -> head -> argmax)
                      captured once into a HIP graph and replayed per token, with
-                     the resident conv/SSM states updated in place.
+                     the resident conv/SSM states updated in place; its prefill
+                     replayed from a GraphPrefill.
+  GraphPrefill       MambaModel.prefill captured once per prompt shape (batch,
+                     seqlen) into a HIP graph and replayed: the per-op host dispatch
+                     of the layer loop (~10 ops per layer) is paid once, at capture.
 """
 
 from __future__ import annotations
@@ -100,6 +104,51 @@ def generate_fast(model, tokenizer, prompt: str, max_new_tokens: int = 50,
     return prompt + tokenizer.decode(generated_ids, skip_special_tokens=True)
 
 
+class GraphPrefill:
+    """``MambaModel.prefill(input_ids, last_only=True)`` replayed from a HIP graph
+    captured once per ``(batch, seqlen)``.
+
+    Calling it copies ``input_ids`` into the graph's input buffer, replays the graph and
+    returns ``(logits (B, 1, vocab), conv_states, ssm_states)`` -- tensors owned by that
+    shape's graph: the same tensors come back from every call of that shape and are
+    overwritten by the next one (copy what must outlive it).  The captured graph runs the
+    same kernels in the same order as the eager prefill (its results are identical); it
+    holds its own memory pool per captured shape (``clear()`` releases them)."""
+
+    def __init__(self, model):
+        self.model = model
+        self._graphs: dict = {}
+
+    def clear(self) -> None:
+        self._graphs.clear()
+
+    def _capture(self, input_ids):
+        ids = input_ids.clone()
+        # Warm up on a side stream first (lazy library init, hipBLASLt heuristics for these
+        # shapes); capturing does not execute anything.
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self.model.prefill(ids, last_only=True)
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            logits, convs, ssms = self.model.prefill(ids, last_only=True)
+        ent = (g, ids, logits, convs, ssms)
+        self._graphs[tuple(input_ids.shape)] = ent
+        return ent
+
+    @torch.inference_mode()
+    def __call__(self, input_ids: torch.Tensor):
+        ent = self._graphs.get(tuple(input_ids.shape))
+        if ent is None:
+            ent = self._capture(input_ids)
+        g, ids, logits, convs, ssms = ent
+        ids.copy_(input_ids)
+        g.replay()
+        return logits, convs, ssms
+
+
 class GraphDecoder:
     """Greedy/sampled decode with the whole step captured in one HIP graph.
 
@@ -108,6 +157,10 @@ class GraphDecoder:
     graph -- embedding, every layer's in-place conv/SSM update, the head and
     argmax -- and returns the next token ids (B,) on the device, with no host
     sync.  Greedy only when captured (``temperature == 0``); sampling runs eagerly.
+    With ``use_graph`` the prefill is replayed from a ``GraphPrefill`` as well: the
+    resident decode state is then the captured prefill's own state buffers for the
+    first prompt shape (a later prompt of that shape writes its state into them
+    directly; other shapes are copied in).
     """
 
     def __init__(self, model, batch_size: int, use_graph: bool = True):
@@ -119,6 +172,7 @@ class GraphDecoder:
         self.next_ids = None
         self.convs = None
         self.ssms = None
+        self.prefill = GraphPrefill(model) if use_graph else None
 
     def _eager_step(self):
         logits, _, _ = self.model.step(self.ids.view(-1, 1), self.convs, self.ssms, inplace=True)
@@ -127,14 +181,18 @@ class GraphDecoder:
     @torch.inference_mode()
     def start(self, input_ids: torch.Tensor) -> torch.Tensor:
         assert input_ids.shape[0] == self.batch
-        logits, convs, ssms = self.model.prefill(input_ids, last_only=True)
+        if self.prefill is not None:
+            logits, convs, ssms = self.prefill(input_ids)
+        else:
+            logits, convs, ssms = self.model.prefill(input_ids, last_only=True)
         first = _argmax(logits[:, -1, :])
         if self.convs is None:
-            self.convs, self.ssms = convs, ssms
+            self.convs, self.ssms = list(convs), list(ssms)
             self.ids = first.clone()
         else:  # keep the captured buffers; copy the new prefill state into them
-            for dst, src in zip(self.convs + self.ssms, convs + ssms):
-                dst.copy_(src)
+            for dst, src in zip(self.convs + self.ssms, list(convs) + list(ssms)):
+                if dst is not src:
+                    dst.copy_(src)
             self.ids.copy_(first)
         if self.use_graph and self.graph is None:
             self._capture()

@@ -128,7 +128,8 @@ class MambaModel(nn.Module):
 
         h = self._run(input_ids, mix)
         if last_only:
-            h = h[:, -1:, :]
+            # (B, d_model) rows: decode-sized row blocks take the weight-streaming head
+            return self._head(h[:, -1, :])[:, None, :], convs, ssms
         return self._head(h), convs, ssms
 
     def step(self, input_ids: torch.Tensor, conv_states, ssm_states, inplace: bool = False):

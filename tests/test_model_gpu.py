@@ -196,6 +196,41 @@ def test_graph_decoder_matches_eager(dev, small):
     assert np.array_equal(generate_fast_ids(model, ids, 12, use_graph=True).cpu().numpy(), eager)
 
 
+@pytest.mark.parametrize("shape", ["130m", "2.8b-width"])
+def test_graph_prefill_matches_eager(dev, shape):
+    """GraphPrefill (MambaModel.prefill captured per prompt shape in a HIP graph) equals the
+    eager prefill bit for bit -- logits and every layer's conv / SSM state -- on four
+    replays with new prompts, with eager prefills of another shape through the same
+    library between the replays.  130m: config 1's full model at its 2048-token prompt
+    (the hipBLASLt projections, the conv, the split-mode scan); 2.8b width: 2 layers at
+    batch 64 x 512 tokens (config 3's prefill shapes, the chained channel-contiguous scan)."""
+    from mamba_metal_amd import GraphPrefill
+    from mamba_metal_amd.selective_scan import reset_scan_status, scan_status
+
+    if shape == "130m":
+        model, cfg = make_model(dev, dtype=torch.float16, seed=21, d_model=768, n_layer=24,
+                                vocab_size=50280, dt_rank=48)
+        B, L = 1, 2048
+    else:
+        model, cfg = make_model(dev, dtype=torch.float16, seed=22, d_model=2560, n_layer=2,
+                                vocab_size=50280, dt_rank=160)
+        B, L = 64, 512
+    rng = np.random.default_rng(21)
+    gp = GraphPrefill(model)
+    reset_scan_status(dev)
+    with torch.inference_mode():
+        for rep in range(4):
+            ids = torch.as_tensor(rng.integers(0, cfg.vocab_size, (B, L)), device=dev)
+            lg, convs, ssms = model.prefill(ids, last_only=True)
+            glg, gconvs, gssms = gp(ids)
+            assert torch.equal(glg, lg), f"replay {rep}: logits differ"
+            for i, (a, b) in enumerate(zip(gconvs + gssms, convs + ssms)):
+                assert torch.equal(a, b), f"replay {rep}: state tensor {i} differs"
+            model.prefill(ids[:, : L // 2 + 3], last_only=True)   # eager work between replays
+            torch.cuda.synchronize()
+    assert scan_status(dev) == 0
+
+
 @pytest.mark.parametrize("batch", [2, 12])
 def test_graph_decoder_fused_paths_match_eager(dev, batch):
     """130m width (3 layers), fp16: the captured decode step with the batch-dependent fused
