@@ -189,17 +189,16 @@ __device__ __forceinline__ float lane_xor(float v, int m) {
   }
 }
 
-// softplus with the reference's cutoff: x <= 20 ? log(1 + exp(x)) : x
-// (selective_scan_chunked.metal:60-65).  log1p is evaluated as
-// log(s) * e / (s - 1) with s = 1 + e (Goldberg's log1p correction) so tiny e
-// keeps full relative precision.
-__device__ __forceinline__ float softplus_cut(float x) {
+// log(1 + exp(x)), the softplus below the reference's cutoff of 20
+// (selective_scan_chunked.metal:60-65; the scan applies the cutoff itself).  log1p is
+// evaluated as log(s) * e / (s - 1) with s = 1 + e (Goldberg's log1p correction) so tiny
+// e keeps full relative precision.
+__device__ __forceinline__ float log1p_exp(float x) {
   const float e = exp2_hw(x * kLog2e);
   const float s = 1.0f + e;
   const float dm = s - 1.0f;
   const float l = log2_hw(s) * kLn2;
-  const float lp = (dm == 0.0f) ? e : l * (e * rcp_hw(dm));
-  return x <= 20.0f ? lp : x;
+  return (dm == 0.0f) ? e : l * (e * rcp_hw(dm));
 }
 
 // softplus without cutoff: log(1 + exp(x)) = max(x, 0) + log1p(exp(-|x|))

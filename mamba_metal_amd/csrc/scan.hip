@@ -73,7 +73,7 @@ struct Params {
   int64_t nunits;     // ncb * nseg
   int64_t us0, us1, us2, ds0, ds1, ds2, zs0, zs1, zs2, ys0, ys1, ys2;
   int64_t As0, As1, Ds;
-  int32_t softplus;
+  float softplus_cut;  // 20 with delta_softplus, NaN without (see delta_log2)
   int32_t vec_ok;
   int* status;  // optional persistent status word (MM_SCAN_STATUS_* bits are ORed in)
   uint64_t spin_ticks;  // hand-off wait bound in wall-clock (s_memrealtime) ticks
@@ -210,14 +210,18 @@ struct Vec<DT, 2> {
   typedef T type __attribute__((ext_vector_type(2)));
 };
 
-// delta2 = softplus(x) * log2(e).  fp32 inputs keep log1p accuracy; fp16/bf16 inputs
-// (whose own rounding is 2^-11 / 2^-8) use log2(1 + 2^m) directly.
+// delta2 = delta' * log2(e), delta' = x <= cut ? softplus(x) : x.  cut is the reference's
+// softplus cutoff 20 when delta_softplus is on, NaN when it is off (every comparison with
+// NaN is false: delta' = x), so the flag costs no select of its own.  fp32 inputs keep
+// log1p accuracy; fp16/bf16 inputs (whose own rounding is 2^-11 / 2^-8) use
+// log2(1 + 2^m) directly.
 template <int DT>
-__device__ __forceinline__ float softplus_log2(float x) {
+__device__ __forceinline__ float delta_log2(float x, float cut) {
   const float m = x * kLog2e;
-  if (DT == MM_F32) return softplus_cut(x) * kLog2e;
-  const float l = log2_hw(1.0f + exp2_hw(m));
-  return x <= 20.0f ? l : m;
+  float l;
+  if constexpr (DT == MM_F32) l = log1p_exp(x) * kLog2e;
+  else l = log2_hw(1.0f + exp2_hw(m));
+  return x <= cut ? l : m;
 }
 
 // ---------------------------------------------------------------------------
@@ -452,6 +456,8 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
                        VE& zA, float4 (&bcA)[BCPT], VE& uB, VE& dB, VE& zB, float4 (&bcB)[BCPT],
                        bool issue) __attribute__((always_inline)) {
       const int64_t t0 = tile * kT;
+      // Tiles wholly inside the tensors (every tile when seqlen and dim are whole tiles
+      // and blocks) skip the masking below on a wave-uniform branch.
       const bool full = (t0 + kT <= p.seqlen) && (d0 + CPW <= p.dim);
 
       // ---- prologue ----
@@ -460,7 +466,7 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
       for (int j = 0; j < EPT; ++j) {
         const float uu = Ty<DT>::f(ru[j]);
         const float dr = Ty<DT>::f(rd[j]);
-        const float d2 = p.softplus ? softplus_log2<DT>(dr) : dr * kLog2e;
+        const float d2 = delta_log2<DT>(dr, p.softplus_cut);
         dtv[j] = d2;
         duv[j] = d2 * uu;
         if constexpr (MODE != kSummary) {
@@ -469,6 +475,9 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
         }
       }
       if (!full) {
+        // The empty volatile asm cannot be speculated, so the compiler keeps this a
+        // branch instead of turning it into selects that every tile would execute.
+        asm volatile("");
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
           const bool in = (d0 + ec(j) < p.dim) && (t0 + et(j) < p.seqlen);
@@ -608,7 +617,7 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
       if constexpr (VEC) {
         T* const yp = static_cast<T*>(y_) + b * p.ys0 + (d0 + vc) * p.ys1 +
                       (LAYOUT == kTimeContig ? t0 + vt : (t0 + vt) * p.ys2);
-        if ((d0 + vc < p.dim) && (t0 + vt < p.seqlen)) *reinterpret_cast<VE*>(yp) = ry;
+        if (full || ((d0 + vc < p.dim) && (t0 + vt < p.seqlen))) *reinterpret_cast<VE*>(yp) = ry;
       } else {
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
@@ -962,7 +971,7 @@ int fwd(const mm_scan_params* a, void* stream, bool chained_min_ok) {
   p.As0 = a->A_stride[0];
   p.As1 = a->A_stride[1];
   p.Ds = a->D_stride;
-  p.softplus = a->delta_softplus ? 1 : 0;
+  p.softplus_cut = a->delta_softplus ? 20.0f : __builtin_nanf("");
   p.vec_ok = vec_ok;
   p.status = a->status;
   {
