@@ -232,13 +232,14 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
     float* __restrict__ state_out_, int* __restrict__ ctl_, float* __restrict__ carry_,
     int* __restrict__ tick_, float* __restrict__ sum_) {
   using T = typename Ty<DT>::T;
-  // CPW channels per workgroup: lane l takes channel l % CPW; with CPW = 32 the two
-  // half-waves take the same channels and different states (HV = 2 state groups per
-  // wave, GS = G * HV in all).
-  static_assert(CPW == 64 || CPW == 32, "channel block");
-  constexpr int HV = 64 / CPW;
-  constexpr int GS = G * HV;
+  // CPW channels per workgroup and GS = 64 G / CPW state groups.  CPW = 64: lane l takes
+  // channel l, wave g state group g.  CPW = 32: the two half-waves take the same
+  // channels and different states (state groups g and g + G).  CPW = 48 (6 waves):
+  // thread t takes channel t % 48 and state group t / 48.
+  static_assert(CPW == 64 || CPW == 48 || CPW == 32, "channel block");
   constexpr int NT = 64 * G;
+  static_assert(NT % CPW == 0, "whole state groups per workgroup");
+  constexpr int GS = NT / CPW;
   constexpr int EPT = CPW * kT / NT;  // elements per thread per tile
   static_assert(EPT == 8 || EPT == 4 || EPT == 2, "tile split");
   using VE = typename Vec<DT, EPT>::type;
@@ -282,8 +283,9 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int g = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lch = lane & (CPW - 1);        // this lane's channel in the block
-  const int sg = (lane / CPW) * G + g;     // this lane's state group (uniform when HV = 1)
+  // this thread's channel in the block and its state group (wave-uniform when CPW = 64)
+  const int lch = (64 % CPW == 0) ? (lane & (CPW - 1)) : (tid % CPW);
+  const int sg = (64 % CPW == 0) ? (lane / CPW) * G + g : (tid / CPW);
   const bool has_z = z_ != nullptr;
 
   // Element ownership for the prologue / epilogue: consecutive threads walk the
@@ -810,6 +812,20 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
     // 768 vs 1.46-1.47 at 512), with fewer the chains' segment order is the critical path
     // and spare workgroups take the next segments early (B=8 D=1536 L=8192: 0.605 ms at
     // 768, 0.627 at 512).
+    // Between one and two 32-channel chains per CU (B=8 D=1536: 384 chains on 256 CUs)
+    // half the CUs would run two chains, which then set the critical path; 48-channel
+    // blocks of 6 waves make it one chain per CU where that many fit (256 there).  The
+    // carries of 48-channel blocks fit the workspace's 64-channel layout when dim rounds
+    // up no further for 48 than for 64.
+    const int64_t ncb48 = a->batch * ceil_div(a->dim, 48);
+    if (p.ncb > cus && ncb48 <= cus && round_up(a->dim, 48) <= round_up(a->dim, 64)) {
+      auto k48 = scan_kernel<DT, LAYOUT, SPL, 6, VEC, kChained, 48>;
+      static DeviceCache c48_cache;
+      const int64_t r48 = cus * resident_per_cu(c48_cache, k48, 64 * 6);
+      set_blocks(p, a->batch, 48);
+      launch_chained<DT, LAYOUT, SPL, 6, VEC, 48>(p, a, s, w, r48);
+      return;
+    }
     if (p.ncb >= 2 * cus && p.ncb < 4 * cus && r32 > 2 * cus) r32 = 2 * cus;
     launch_chained<DT, LAYOUT, SPL, GS / 2, VEC, 32>(p, a, s, w, r32);
   } else {

@@ -196,6 +196,16 @@ def test_layouts(oracle_lib, dev, layout, dtype):
     check(oracle_lib, dev, inp, f"layout {layout}", dtype=dtype, softplus=True, layout=layout)
 
 
+@pytest.mark.parametrize("layout", ["bdl", "bld"])
+def test_48_channel_blocks(oracle_lib, dev, layout):
+    """B=8 D=1536 (384 32-channel chains, 256 48-channel ones on 256 CUs) runs the 48-channel
+    blocks of 6 waves (thread t: channel t % 48, state group t / 48), time- and
+    channel-contiguous; a 300-step sequence ends inside a tile."""
+    inp = fp16_inputs(8, 1536, 16, 300, seed=48)
+    check(oracle_lib, dev, inp, f"48-channel blocks {layout}", dtype=torch.float16, softplus=True,
+          layout=layout)
+
+
 def test_channel_contiguous_views_keep_their_layout(oracle_lib, dev):
     """Transposed (batch, seqlen, dim) views in: y comes back in the same layout (so the
     kernel's channel-contiguous path runs end to end) with the oracle's values."""
