@@ -14,6 +14,7 @@
 // The decode step replaces mamba_block.py:170-177: shift the (batch, dim, width)
 // window left in place, append x, dot with the taps, add bias, SiLU.
 #include <algorithm>
+#include <type_traits>
 
 #include "mm_common.h"
 
@@ -34,6 +35,7 @@ struct Params {
   int64_t batch, seqlen, dim, width, tc, nchunks, ncg;
   int64_t xs0, xs1, xs2, os0, os1, os2, ws0, ws1;
   int32_t w_dtype, apply_silu, vec_ok;
+  int32_t w_vec;  // 2-byte taps in contiguous rows of 4 (and bias) on 16-byte boundaries
 };
 
 __device__ __forceinline__ float ld_any(const void* p, int64_t i, int32_t dt) {
@@ -57,51 +59,99 @@ __global__ __launch_bounds__(kBlock) void conv1d_kernel(const Params p) {
   const int off = W - static_cast<int>(K > 0 ? K : p.width);  // leading zero taps (K == 0)
 
   // Taps (zero-padded at the old end when K == 0) and bias ((dim,) contiguous, w_dtype).
+  // Every load is unconditional, from a clamped in-bounds address, and masked afterwards:
+  // guarded loads compiled to one branch and one vmcnt(0) wait per tap (~40 dependent
+  // round trips per thread, most of a short sequence's time).  The dtype dispatch is
+  // hoisted out of the loops for the same reason.
   float w[kCV][W], bias[kCV];
+  auto load_taps = [&](auto wdt) __attribute__((always_inline)) {
+    constexpr int WDT = decltype(wdt)::value;
+#pragma unroll
+    for (int j = 0; j < kCV; ++j) {
+      const int64_t c = c0 + j;
+      const int64_t cc = c < p.dim ? c : 0;
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        const int kk = k - off;
+        w[j][k] = ld<WDT>(p.w, cc * p.ws0 + (kk >= 0 ? kk : 0) * p.ws1);
+      }
+      bias[j] = ld<WDT>(p.bias != nullptr ? p.bias : p.w, p.bias != nullptr ? cc : 0);
+    }
+  };
+  // Width 4 with 2-byte taps in contiguous (dim, 4) rows (the model's conv1d.weight): the
+  // thread's 8 channels x 4 taps are 64 contiguous bytes, read as four 16-byte loads, and
+  // its 8 biases as one.
+  auto load_taps_vec = [&](auto wdt) __attribute__((always_inline)) {
+    constexpr int WDT = decltype(wdt)::value;
+    using WV = typename Ty<WDT>::V8;
+    const int64_t cb = c0 < p.dim ? c0 : 0;
+    const WV* const wv = reinterpret_cast<const WV*>(static_cast<const typename Ty<WDT>::T*>(p.w) + cb * 4);
+    const WV r0 = wv[0], r1 = wv[1], r2 = wv[2], r3 = wv[3];
+    const WV rb = *reinterpret_cast<const WV*>(static_cast<const typename Ty<WDT>::T*>(
+        p.bias != nullptr ? p.bias : p.w) + (p.bias != nullptr ? cb : 0));
+    const WV rr[4] = {r0, r1, r2, r3};
+#pragma unroll
+    for (int j = 0; j < kCV; ++j) {
+#pragma unroll
+      for (int k = 0; k < W; ++k) w[j][k] = Ty<WDT>::f(rr[(j * 4 + k) / 8][(j * 4 + k) % 8]);
+      bias[j] = Ty<WDT>::f(rb[j]);
+    }
+  };
+  bool taps_done = false;
+  if constexpr (K == 4) {
+    if (p.w_vec) {
+      if (p.w_dtype == MM_F16) load_taps_vec(std::integral_constant<int, MM_F16>{});
+      else load_taps_vec(std::integral_constant<int, MM_BF16>{});
+      taps_done = true;
+    }
+  }
+  if (!taps_done) {
+    if (p.w_dtype == MM_F32) load_taps(std::integral_constant<int, MM_F32>{});
+    else if (p.w_dtype == MM_F16) load_taps(std::integral_constant<int, MM_F16>{});
+    else load_taps(std::integral_constant<int, MM_BF16>{});
+  }
 #pragma unroll
   for (int j = 0; j < kCV; ++j) {
-    const int64_t c = c0 + j;
-    const bool cin = c < p.dim;
+    const bool cin = c0 + j < p.dim;
 #pragma unroll
-    for (int k = 0; k < W; ++k) {
-      const int kk = k - off;
-      w[j][k] = (cin && kk >= 0) ? ld_any(p.w, c * p.ws0 + kk * p.ws1, p.w_dtype) : 0.0f;
-    }
-    bias[j] = (cin && p.bias) ? ld_any(p.bias, c, p.w_dtype) : 0.0f;
+    for (int k = 0; k < W; ++k) w[j][k] = (cin && k >= off) ? w[j][k] : 0.0f;
+    bias[j] = (cin && p.bias != nullptr) ? bias[j] : 0.0f;
   }
 
   // x[b, t, c0 .. c0 + 7] (t >= 0); channels past dim read as zero.
+  // Unconditional loads here too: on the vector path every thread's channel group lies
+  // inside dim (dim % 8 == 0); the strided path reads channel 0 past dim and masks.
   auto load_x = [&](int64_t t, float v[kCV]) {
     const T* xp = static_cast<const T*>(p.x) + b * p.xs0 + t * p.xs1;
     if constexpr (VEC) {
-      if (c0 < p.dim) {
-        const V8 r = *reinterpret_cast<const V8*>(xp + c0);
+      const V8 r = *reinterpret_cast<const V8*>(xp + c0);
 #pragma unroll
-        for (int j = 0; j < kCV; ++j) v[j] = Ty<DT>::f(r[j]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < kCV; ++j) v[j] = 0.0f;
-      }
+      for (int j = 0; j < kCV; ++j) v[j] = Ty<DT>::f(r[j]);
     } else {
+      float raw[kCV];
 #pragma unroll
-      for (int j = 0; j < kCV; ++j) v[j] = (c0 + j < p.dim) ? Ty<DT>::f(xp[(c0 + j) * p.xs2]) : 0.0f;
+      for (int j = 0; j < kCV; ++j) raw[j] = Ty<DT>::f(xp[(c0 + j < p.dim ? c0 + j : 0) * p.xs2]);
+#pragma unroll
+      for (int j = 0; j < kCV; ++j) v[j] = (c0 + j < p.dim) ? raw[j] : 0.0f;
     }
   };
 
   const int64_t t_begin = chunk * p.tc;
   const int64_t t_end = std::min<int64_t>(t_begin + p.tc, p.seqlen);
 
-  // win[k] holds x[t - (W-1) + k] for k < W-1 (the causal history).
+  // win[k] holds x[t - (W-1) + k] for k < W-1 (the causal history): loaded from step 0
+  // where t < 0 (unconditional loads, see the taps) and zeroed after.
   float win[W > 1 ? W - 1 : 1][kCV];
 #pragma unroll
   for (int k = 0; k < W - 1; ++k) {
     const int64_t t = t_begin - (W - 1) + k;
-    if (t >= 0) {
-      load_x(t, win[k]);
-    } else {
+    load_x(t >= 0 ? t : 0, win[k]);
+  }
 #pragma unroll
-      for (int j = 0; j < kCV; ++j) win[k][j] = 0.0f;
-    }
+  for (int k = 0; k < W - 1; ++k) {
+    const bool tin = t_begin - (W - 1) + k >= 0;
+#pragma unroll
+    for (int j = 0; j < kCV; ++j) win[k][j] = tin ? win[k][j] : 0.0f;
   }
 
   // Vector path: the group's raw 16-byte rows are loaded before any is converted (every
@@ -317,6 +367,10 @@ int mm_causal_conv1d_fwd(const void* x, const void* weight, const void* bias, vo
                  ? 1
                  : 0;
   p.ncg = ceil_div(dim, kCV);
+  p.w_vec = (width == 4 && w_dtype != MM_F32 && p.ws1 == 1 && p.ws0 == 4 && dim % kCV == 0 &&
+             aligned(weight, 16) && (bias == nullptr || aligned(bias, 16)))
+                ? 1
+                : 0;
   // Run length: enough runs for >= ~256k threads (~16 waves per CU), runs of at most
   // 256 steps and at least kU (one load group; the (width-1)-step halo is re-read per run).
   int64_t tc = 256;
