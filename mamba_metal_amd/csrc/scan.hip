@@ -20,7 +20,10 @@
 //     writes the state and raises its own flag.  Every predecessor was claimed earlier
 //     by a resident workgroup, so the wait always ends; the spin is bounded anyway.
 //     Segment-major units balance any number of chains over the CUs.  With few chains
-//     the split mode (see Mode) replaces the hand-off by segment summaries.
+//     the split mode (see Mode) replaces the hand-off by segment summaries; its units
+//     never wait, so its workgroups take them by a static stride (unit = workgroup +
+//     k * grid) instead of the ticket atomic, which all workgroups of a short launch
+//     would contend for at once.
 //   * Per 32-step tile the workgroup runs a prologue over its (channel, time) elements
 //     -- coalesced vector loads of u, delta, z along whichever axis is contiguous,
 //     softplus, delta*u, D*u, SiLU(z) -- and stages delta', delta'*u and the tile's B/C
@@ -297,12 +300,20 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
   auto ec = [&](int j) { return (LAYOUT == kTimeContig) ? vc : vc + j; };
   auto et = [&](int j) { return (LAYOUT == kTimeContig) ? vt + j : vt; };
 
-  for (;;) {
-    // ---- claim a unit (segment-major tickets) ----
-    if (tid == 0) s_ticket = atomicAdd(tick_, 1);
-    __syncthreads();
-    const int64_t unit = s_ticket;
-    __syncthreads();
+  for (int64_t round = 0;; ++round) {
+    // ---- claim a unit: segment-major tickets where units wait for their predecessors
+    // (every predecessor is then claimed by a running workgroup first); the split
+    // passes never wait, and take units by a static stride instead of a contended
+    // device-scope atomic ----
+    int64_t unit;
+    if constexpr (MODE == kChained) {
+      if (tid == 0) s_ticket = atomicAdd(tick_, 1);
+      __syncthreads();
+      unit = s_ticket;
+      __syncthreads();
+    } else {
+      unit = static_cast<int64_t>(blockIdx.x) + round * gridDim.x;
+    }
     if (unit >= p.nunits) break;
     const int64_t cb = unit % p.ncb;
     const int64_t seg = unit / p.ncb;
