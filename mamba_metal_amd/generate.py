@@ -169,14 +169,17 @@ class GraphDecoder:
         self.use_graph = use_graph
         self.graph = None
         self.ids = None
-        self.next_ids = None
         self.convs = None
         self.ssms = None
         self.prefill = GraphPrefill(model) if use_graph else None
 
     def _eager_step(self):
+        """One decode step whose greedy ids overwrite ``self.ids`` (the step's own input,
+        read by the embedding before the argmax writes it)."""
         logits, _, _ = self.model.step(self.ids.view(-1, 1), self.convs, self.ssms, inplace=True)
-        return _argmax(logits[:, 0, :])
+        row = logits[:, 0, :]
+        argmax_rows(row if row.stride(-1) == 1 else row.contiguous(), out=self.ids)
+        return self.ids
 
     @torch.inference_mode()
     def start(self, input_ids: torch.Tensor) -> torch.Tensor:
@@ -201,29 +204,30 @@ class GraphDecoder:
     def _capture(self):
         # Warm up on a side stream (lazy library init, hipBLASLt heuristics), then
         # restore the state the warm-up step advanced.
-        saved = [t.clone() for t in self.convs + self.ssms]
+        saved = [t.clone() for t in self.convs + self.ssms + [self.ids]]
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             self._eager_step()
         torch.cuda.current_stream().wait_stream(s)
-        for dst, src in zip(self.convs + self.ssms, saved):
+        for dst, src in zip(self.convs + self.ssms + [self.ids], saved):
             dst.copy_(src)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self.next_ids = self._eager_step()
+            self._eager_step()  # the argmax writes the next step's input ids in place
         # Capturing does not execute; the state is still the prefill state.
         self.graph = g
 
     @torch.inference_mode()
     def step(self) -> torch.Tensor:
-        """Advance every sequence by one token; returns the next ids (B,)."""
+        """Advance every sequence by one token; returns the next ids (B,).
+
+        The returned tensor is the decoder's own input buffer: the next step overwrites it
+        (clone what must be kept)."""
         if self.graph is not None:
             self.graph.replay()
-            self.ids.copy_(self.next_ids)
-            return self.ids
-        nxt = self._eager_step()
-        self.ids.copy_(nxt)
+        else:
+            self._eager_step()
         return self.ids
 
 
