@@ -328,6 +328,19 @@ int mm_decode_in_proj_xproj(const mm_linear_params* params, const void* xp_w_pac
                             int64_t xp_n, void* xp_y, int64_t ld_xp, void* stream);
 
 /* ------------------------------------------------------------------------- */
+/* Prefill projection GEMM for short K -- replaces the dt projection of the parallel
+ * prefill (MambaBlock.prefill, mamba_block.py:136: dt_proj with its bias, K = dt_rank):
+ *   y[m, n] = round(sum_k x[m, k] * w[n, k] + bias[n])     (fp32 accumulation)
+ * x (M, K) row stride ldx; w nn.Linear's (N, K) weight, row stride ldw (not packed);
+ * bias (N,) or NULL; y (M, N) row stride ldy.  f16 / bf16, one dtype for every tensor;
+ * K a multiple of 16; ldx and ldw multiples of 8; x and w 16-byte aligned.  Operands go
+ * straight from memory to the matrix cores: any K is computed correctly, but only short
+ * K (up to a few hundred) is faster than a library GEMM.  No workspace. */
+int mm_prefill_linear(const void* x, const void* w, const void* bias, void* y, int64_t M,
+                      int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, int32_t dtype,
+                      void* stream);
+
+/* ------------------------------------------------------------------------- */
 /* Greedy token choice -- replaces `mx.argmax(logits[:, -1, :], axis=-1)` of
  * generate_fast (generate.py:91-93): out[r] = index of the largest x[r, 0:n]
  * (lowest index on ties, a NaN beats every number).  x rows of stride >= n in

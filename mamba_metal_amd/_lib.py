@@ -105,6 +105,7 @@ _SIGNATURES = {
     "mm_decode_in_proj_xproj_workspace_size": ([_i64] * 5, _sz),
     "mm_decode_in_proj_xproj": ([ctypes.POINTER(LinearParams), _vp, _i64, _vp, _i64, _vp],
                                 ctypes.c_int),
+    "mm_prefill_linear": ([_vp] * 4 + [_i64] * 6 + [_i32, _vp], ctypes.c_int),
     "mm_argmax_rows": ([_vp, _i64, _i64, _i64, _i32, _vp, _vp], ctypes.c_int),
     "mm_pair_scan": ([_vp] * 4 + [_i64, _vp], ctypes.c_int),
 }

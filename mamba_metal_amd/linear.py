@@ -260,3 +260,54 @@ def decode_in_proj_conv(x, w, conv_state, conv_w, conv_b=None, x_norm=None):
     prm.n_conv = n_conv
     _call(prm, dev)
     return x_conv, z
+
+
+# ---------------------------------------------------------------- prefill projections
+# mm_prefill_linear, the matrix-core GEMM for short K (the dt projection, K = dt_rank),
+# takes prefill calls up to these sizes; deeper or larger products stay on torch's GEMM.
+PREFILL_MAX_K = 256
+PREFILL_MAX_M = 4096
+
+
+def _prefill_operands_ok(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None) -> bool:
+    return (x.is_cuda and x.dim() == 2 and w.dim() == 2 and x.dtype in (torch.float16, torch.bfloat16)
+            and w.dtype == x.dtype and w.device == x.device and x.shape[1] == w.shape[1]
+            and x.shape[1] % 16 == 0 and x.stride(1) == 1 and w.stride(1) == 1
+            and x.stride(0) % 8 == 0 and w.stride(0) % 8 == 0
+            and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0
+            and (bias is None or (bias.dtype == x.dtype and bias.device == x.device
+                                  and tuple(bias.shape) == (w.shape[0],) and bias.stride(0) == 1)))
+
+
+def prefill_linear_ok(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None) -> bool:
+    """Whether a prefill projection should run on ``prefill_linear``: operands it takes
+    (2-D x with unit column stride, f16/bf16, K a multiple of 16, 16-byte aligned rows)
+    and short K (<= PREFILL_MAX_K, M <= PREFILL_MAX_M), where it beats torch's GEMM."""
+    return (x.dim() == 2 and x.shape[0] <= PREFILL_MAX_M and x.shape[1] <= PREFILL_MAX_K
+            and _prefill_operands_ok(x, w, bias))
+
+
+def prefill_linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x @ w.T (+ bias) for x (M, K) and nn.Linear's (N, K) weight with short K, on
+    the library's matrix-core kernel (mm_prefill_linear); returns (M, N) in x's dtype."""
+    lib = _lib.load()
+    dev = _lib.require_cuda(x, w, bias, out)
+    if not _prefill_operands_ok(x, w, bias):
+        raise ValueError("prefill_linear: x (M, K) and w (N, K) must be f16/bf16 on one GPU with unit "
+                         "column stride, K a multiple of 16, 16-byte aligned rows; bias (N,)")
+    M, K = x.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=x.dtype, device=dev)
+    if out.shape != (M, N) or out.dtype != x.dtype or out.stride(1) != 1:
+        raise ValueError("out must be an (M, N) tensor of x's dtype with unit column stride")
+    if M == 0 or N == 0:
+        return out
+    with _lib.on_device(dev):
+        st = lib.mm_prefill_linear(x.data_ptr(), w.data_ptr(),
+                                   bias.data_ptr() if bias is not None else None, out.data_ptr(),
+                                   M, N, K, x.stride(0), w.stride(0), out.stride(0),
+                                   _lib.dtype_code(x.dtype), _lib.stream_of(dev))
+    _lib.check(st, "mm_prefill_linear")
+    return out

@@ -16,9 +16,10 @@ Where the reference transposes activations to (B, dim, L) contiguous copies
 before the scan (mamba_block.py:90-100), this block hands the kernel strided
 (B, L, dim) views: the scan reads channel-contiguous tiles directly.
 
-Prefill GEMMs (in/x/dt/out projections) run on torch (hipBLASLt); the conv, the
-scan and every decode-step op -- including the projections at decode batch <= 64,
-on the weight-streaming GEMM -- are libmamba_mi355x kernels.
+The prefill's in/x/out projections run on torch (hipBLASLt) and its dt projection
+(K = dt_rank, with bias) on the library's short-K matrix-core GEMM (mm_prefill_linear);
+the conv, the scan and every decode-step op -- including the projections at decode
+batch <= 64, on the weight-streaming GEMM -- are libmamba_mi355x kernels.
 """
 
 from __future__ import annotations
@@ -34,12 +35,13 @@ from mamba_metal_amd.decode import ssm_step_dtproj
 from mamba_metal_amd.linear import (NORM_IN_MAX_M, decode_in_proj_conv, decode_in_proj_conv_xproj,
                                     decode_linear, decode_linear_ok, decode_linear_resid_,
                                     decode_linear_resid_norm_, in_proj_conv_ok, norm_in_ok,
-                                    split_k, xproj_weight_ok)
+                                    prefill_linear, prefill_linear_ok, split_k, xproj_weight_ok)
 from mamba_metal_amd.norm import add_rmsnorm
 from mamba_metal_amd.selective_scan import selective_scan_into
 
 # step_2d's marker for "resid updated, next norm not applied yet" (see step_2d).
 NORM_PENDING = object()
+
 
 
 class MambaBlock(nn.Module):
@@ -97,9 +99,12 @@ class MambaBlock(nn.Module):
         # with row stride dt_rank + 2N), bias in the GEMM epilogue: F.linear on the
         # non-contiguous 3-D slice added the bias in a separate pass over (B, L, d_inner).
         dt_2d = dt_pre.reshape(Bsz * L, -1)
-        W_dt = self.dt_proj.weight.t()
-        dt = (torch.addmm(self.dt_proj.bias, dt_2d, W_dt) if self.dt_proj.bias is not None
-              else dt_2d @ W_dt).view(Bsz, L, di)
+        if prefill_linear_ok(dt_2d, self.dt_proj.weight, self.dt_proj.bias):
+            dt = prefill_linear(dt_2d, self.dt_proj.weight, self.dt_proj.bias).view(Bsz, L, di)
+        else:
+            W_dt = self.dt_proj.weight.t()
+            dt = (torch.addmm(self.dt_proj.bias, dt_2d, W_dt) if self.dt_proj.bias is not None
+                  else dt_2d @ W_dt).view(Bsz, L, di)
         y = torch.empty_like(x_main)
         selective_scan_into(x_main.transpose(1, 2), dt.transpose(1, 2), self._A(),
                             Bm.transpose(1, 2), Cm.transpose(1, 2), y.transpose(1, 2),
