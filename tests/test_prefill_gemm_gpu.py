@@ -48,9 +48,10 @@ def _check(got, x, w, b, dtype, what):
 ])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_prefill_linear(M, K, N, ldx, bias, dtype):
-    from mamba_metal_amd.linear import PREFILL_MAX_K, prefill_linear, prefill_linear_ok
+    from mamba_metal_amd.linear import PREFILL_MAX_K, PREFILL_MAX_M, prefill_linear, prefill_linear_ok
     x, w, b = _inputs(M, K, N, dtype, seed=M + N, ldx=ldx, bias=bias)
-    assert prefill_linear_ok(x, w, b) == (K <= PREFILL_MAX_K)  # the model routes short K here
+    # the model routes short K (and M up to the cap) here; every case is computed either way
+    assert prefill_linear_ok(x, w, b) == (K <= PREFILL_MAX_K and M <= PREFILL_MAX_M)
     y = prefill_linear(x, w, b)
     torch.cuda.synchronize()
     _check(y, x, w, b, dtype, f"prefill_linear M={M} K={K} N={N}")
