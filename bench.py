@@ -25,7 +25,7 @@ resident in HBM.  A step is one ``selective_scan`` call (B/C pack + scan kernel)
                 (config 3) random-init models.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-decode] [--no-cpu]
-       python bench.py --only-scan [config4|config2|reference] | --only-gemm [store|conv_xp]
+       python bench.py --only-scan [config4|config2|reference] | --only-gemm [store|conv|conv_xp]
                        | --only-decode {130m,2.8b} | --copy-probe-only   (profiling commands)
 """
 
@@ -355,15 +355,17 @@ def decode_bench(name, cfg_kw, batch, prompt_len, n_decode, seed=0):
     return res
 
 
-def gemm_probe(calls=24, n_weights=12, fused=False):
+def gemm_probe(calls=24, n_weights=12, mode="store"):
     """The decode GEMM at Mamba-2.8B's in_proj shape (M=64, K=2560, N=10240 fp16), weights
-    rotated so each call streams its 52 MB from HBM; HIP-event average per call.  fused:
-    in_proj + conv window + x_proj (mm_decode_in_proj_xproj) exactly as the decode step
-    runs it -- the in_proj kernel with the CONV and x_proj-partial epilogue, then the
-    x_proj plane reduce."""
+    rotated so each call streams its 52 MB from HBM; HIP-event average per call.  mode
+    "store": the plain product (mm_decode_linear); "conv": in_proj + conv window
+    (mm_decode_linear, CONV epilogue); "conv_xp": in_proj + conv window + x_proj
+    (mm_decode_in_proj_xproj) exactly as the decode step runs it -- the in_proj kernel with
+    the CONV and x_proj-partial epilogue, then the x_proj plane reduce."""
     import torch
 
-    from mamba_metal_amd.linear import decode_in_proj_conv_xproj, decode_linear, packed_weight
+    from mamba_metal_amd.linear import (decode_in_proj_conv, decode_in_proj_conv_xproj, decode_linear,
+                                        packed_weight)
 
     dev = torch.device("cuda:0")
     M, K, N = 64, 2560, 10240
@@ -374,14 +376,17 @@ def gemm_probe(calls=24, n_weights=12, fused=False):
         packed_weight(w)
     x = torch.randn((M, K), generator=g, device=dev).half()
     out = torch.empty((M, N), device=dev, dtype=torch.float16)
-    if fused:
+    if mode != "store":
         di = N // 2
         conv_state = torch.zeros((M, di, 4), device=dev, dtype=torch.float16)
         conv_w = (torch.randn((di, 1, 4), generator=g, device=dev) * 0.5).half()
         conv_b = torch.zeros(di, device=dev, dtype=torch.float16)
         w_x = (torch.randn((160 + 32, di), generator=g, device=dev) * 0.02).half()
         packed_weight(w_x)
-        run = lambda i: decode_in_proj_conv_xproj(x, ws[i % n_weights], conv_state, conv_w, conv_b, w_x)
+        if mode == "conv_xp":
+            run = lambda i: decode_in_proj_conv_xproj(x, ws[i % n_weights], conv_state, conv_w, conv_b, w_x)
+        else:
+            run = lambda i: decode_in_proj_conv(x, ws[i % n_weights], conv_state, conv_w, conv_b)
     else:
         run = lambda i: decode_linear(x, ws[i % n_weights], out=out)
     for i in range(3):
@@ -394,7 +399,8 @@ def gemm_probe(calls=24, n_weights=12, fused=False):
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / calls
-    name = "decode in_proj + conv + x_proj" if fused else "decode in_proj"
+    name = {"store": "decode in_proj", "conv": "decode in_proj + conv",
+            "conv_xp": "decode in_proj + conv + x_proj"}[mode]
     return {"gemm": f"{name} M=64 K=2560 N=10240 fp16", "us_per_call": us,
             "weight_gbs": N * K * 2 / us / 1e3, "calls": calls}
 
@@ -426,9 +432,10 @@ def main():
     ap.add_argument("--only-scan", nargs="?", const="config4",
                     choices=["config4", "config2", "reference"],
                     help="one scan only (the command the committed rocprof summaries use)")
-    ap.add_argument("--only-gemm", nargs="?", const="store", choices=["store", "conv_xp"],
+    ap.add_argument("--only-gemm", nargs="?", const="store", choices=["store", "conv", "conv_xp"],
                     help="a decode GEMM at the 2.8B in_proj shape only (counter profiles): the "
-                         "plain kernel, or in_proj + conv window + x_proj partials as decode runs it")
+                         "plain kernel, in_proj + conv window, or in_proj + conv window + x_proj "
+                         "partials as decode runs it")
     args = ap.parse_args()
     if args.only_scan and args.only_scan != "config4":
         import torch
@@ -455,7 +462,7 @@ def main():
 
     if args.only_gemm:
         _lib.load()
-        print(json.dumps(gemm_probe(fused=args.only_gemm == "conv_xp")))
+        print(json.dumps(gemm_probe(mode=args.only_gemm)))
         return
     if args.only_decode:
         _lib.load()
