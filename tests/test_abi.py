@@ -279,6 +279,27 @@ def test_argmax_validation(lib):
     assert lib.mm_argmax_rows(FAKE, 0, 8, 8, _lib.F16, out, None) == _lib.OK
 
 
+def test_prefill_linear_validation(lib):
+    f = lib.mm_prefill_linear  # x, w, bias, y, M, N, K, ldx, ldw, ldy, dtype, stream
+    ok = dict(M=4, N=4, K=16, ldx=16, ldw=16, ldy=4, dt=_lib.F16)
+
+    def call(x=FAKE, w=FAKE, y=FAKE, **kw):
+        a = {**ok, **kw}
+        return f(x, w, None, y, a["M"], a["N"], a["K"], a["ldx"], a["ldw"], a["ldy"], a["dt"], None)
+
+    assert call(x=None) == _lib.ERR_NULL_POINTER
+    assert call(y=None) == _lib.ERR_NULL_POINTER
+    assert call(dt=_lib.F32) == _lib.ERR_DTYPE              # f16 / bf16 only
+    assert call(M=-1) == _lib.ERR_SHAPE
+    assert call(K=24, ldx=24, ldw=24) == _lib.ERR_SHAPE     # K not a multiple of 16
+    assert call(ldx=8) == _lib.ERR_LAYOUT                   # row stride below K
+    assert call(ldy=2) == _lib.ERR_LAYOUT                   # output row stride below N
+    assert call(ldx=20) == _lib.ERR_LAYOUT                  # rows not 16-byte aligned
+    assert call(w=FAKE + 2) == _lib.ERR_LAYOUT              # misaligned base
+    assert call(M=0) == _lib.OK                             # nothing to do
+    assert call(N=0, ldy=0) == _lib.OK
+
+
 def test_zero_sizes_are_noops(lib):
     # Nothing to do -> MM_OK without touching the (fake) pointers or the device.
     assert _scan(lib, batch=0) == _lib.OK
