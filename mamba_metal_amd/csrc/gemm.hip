@@ -856,16 +856,20 @@ __global__ __launch_bounds__(256) void reduce_norm_kernel(const LinParams p) {
 // t/16, t/16 + 16, ...: in the packed layout each 16-thread group reads two contiguous
 // 128-byte pieces per step.  Each thread accumulates in k order in fp32; the 32 threads
 // of a column are combined by an xor-shuffle tree (within a wave) and then in wave
-// order through LDS -- deterministic.  Loads run kGvU steps ahead of their use
-// (clamped to the last step: every load is in bounds and unconditional).  The input
+// order through LDS -- deterministic.  Loads are issued U steps at a time ahead of their
+// use (clamped to the last step: every load is in bounds and unconditional, and a clamped
+// step is multiplied in with a zero weight).  U (3 or 4) is picked per call from the steps
+// per thread, T = ceil(K / 16 / 16): fewest load rounds, then fewest clamped steps -- at
+// the Mamba-130M shapes (T = 3 and 6) U = 3 wastes none where U = 4 wasted one or two per
+// round (130M decode 0.370-0.382 -> 0.364 ms per step; U = 2, 6, 8 measured 0.40, 0.39,
+// 0.42 ms).  The input
 // RMSNorm (NORM) is computed by wave 0 in add_rmsnorm_vec_kernel's order and applied as
 // each x chunk is loaded, as in linear_kernel.  Epilogues as the split-K reduce.
 constexpr int kGvCols = 8;
 constexpr int kGvThreads = 256;
 constexpr int kGvMaxM = 4;
-constexpr int kGvU = 4;
 
-template <int DT, int MM, int EPI, bool NORM>
+template <int DT, int MM, int EPI, bool NORM, int U>
 __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
   using T = typename Ty<DT>::T;
   using V8 = typename Ty<DT>::V8;
@@ -888,11 +892,11 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
   // Load group at steps sb, sb + 16, ... (clamped to the last step; steps past the end
   // count with a zero weight when consumed).
   const int64_t s_last = nsteps - 1;
-  u32x4 wv[kGvU], nv[kGvU];
-  V8 xv[kGvU][MM];
+  u32x4 wv[U], nv[U];
+  V8 xv[U][MM];
   auto load = [&](int64_t sb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < kGvU; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t st = sb + 16 * u < nsteps ? sb + 16 * u : s_last;
       wv[u] = wb[st * 64];
 #pragma unroll
@@ -928,7 +932,7 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
     // Consuming every loaded step (a zero weight past the end) keeps the compiler from
     // sinking the loads behind a branch.
 #pragma unroll
-    for (int u = 0; u < kGvU; ++u) {
+    for (int u = 0; u < U; ++u) {
       const u32x4 zero = {0u, 0u, 0u, 0u};
       const V8 w8 = __builtin_bit_cast(V8, sb + 16 * u < nsteps ? wv[u] : zero);
 #pragma unroll
@@ -942,7 +946,7 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
         }
       }
     }
-    sb += 16 * kGvU;
+    sb += 16 * U;
     if (sb >= nsteps) break;
     load(sb);
   }
@@ -964,20 +968,34 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
   }
 }
 
-template <int DT, int MM, bool NORM>
-void launch_gemv_e(const LinParams& p, int32_t epi, hipStream_t s) {
+template <int DT, int MM, bool NORM, int U>
+void launch_gemv_u(const LinParams& p, int32_t epi, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(ceil_div(p.N, kGvCols)));
   switch (epi) {
     case MM_LIN_STORE:
-      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_STORE, NORM>), grid, dim3(kGvThreads), 0, s, p);
+      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_STORE, NORM, U>), grid, dim3(kGvThreads), 0, s, p);
       break;
     case MM_LIN_RESID:
-      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_RESID, NORM>), grid, dim3(kGvThreads), 0, s, p);
+      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_RESID, NORM, U>), grid, dim3(kGvThreads), 0, s, p);
       break;
     default:
-      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_CONV, NORM>), grid, dim3(kGvThreads), 0, s, p);
+      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_CONV, NORM, U>), grid, dim3(kGvThreads), 0, s, p);
       break;
   }
+}
+
+// Steps loaded per round (see gemv_kernel): fewest rounds, then fewest clamped steps.
+inline int gemv_group(int64_t K) {
+  const int64_t t = ceil_div(K / kStepK, 16);  // steps per thread
+  const int64_t r3 = ceil_div(t, 3), r4 = ceil_div(t, 4);
+  if (r4 < r3) return 4;
+  return (r3 * 3 - t) < (r4 * 4 - t) ? 3 : 4;
+}
+
+template <int DT, int MM, bool NORM>
+void launch_gemv_e(const LinParams& p, int32_t epi, hipStream_t s) {
+  if (gemv_group(p.K) == 3) launch_gemv_u<DT, MM, NORM, 3>(p, epi, s);
+  else launch_gemv_u<DT, MM, NORM, 4>(p, epi, s);
 }
 
 template <int DT>
