@@ -370,12 +370,18 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
 
     load(wa, xa, na, c_begin);
     if constexpr (NORM) input_norm();
-    for (int64_t c = c_begin; c < c_end; c += 2) {
+    // The last one or two chunks are peeled off: the loop body's prefetch of chunk c + 2
+    // would re-read the last chunk once more (measured: 2.8B decode 3.665 -> 3.642 ms).
+    int64_t c = c_begin;
+    for (; c + 2 < c_end; c += 2) {
       load(wb, xb, nb, c + 1);
       compute(wa, xa, na, c);
       load(wa, xa, na, c + 2);
       compute(wb, xb, nb, c + 1);
     }
+    load(wb, xb, nb, c + 1);
+    compute(wa, xa, na, c);
+    compute(wb, xb, nb, c + 1);
   }
 
   if constexpr (EPI == kPartial) {
@@ -675,13 +681,40 @@ __global__ __launch_bounds__(NW * 64, 1) void share_kernel(const LinParams p) {
   S s0, s1, s2;
   load(s0, cbeg);
   load(s1, cbeg + 1);
-  for (int64_t c = cbeg; c < nchunks; c += 3) {
+  // Whole rounds while all three prefetches stay in range, then the last 1-4 chunks
+  // straight-line: the round's prefetches of c + 3 and c + 4 would otherwise re-read
+  // the last chunk up to four more times.
+  int64_t c = cbeg;
+  for (; c + 4 < nchunks; c += 3) {
     load(s2, c + 2);
     compute(s0, c, 0);
     load(s0, c + 3);
     compute(s1, c + 1, 1);
     load(s1, c + 4);
     compute(s2, c + 2, 2);
+  }
+  switch (nchunks - c) {  // uniform over the workgroup
+    case 4:
+      load(s2, c + 2);
+      compute(s0, c, 0);
+      load(s0, c + 3);
+      compute(s1, c + 1, 1);
+      compute(s2, c + 2, 2);
+      compute(s0, c + 3, 0);
+      break;
+    case 3:
+      load(s2, c + 2);
+      compute(s0, c, 0);
+      compute(s1, c + 1, 1);
+      compute(s2, c + 2, 2);
+      break;
+    case 2:
+      compute(s0, c, 0);
+      compute(s1, c + 1, 1);
+      break;
+    default:
+      compute(s0, c, 0);
+      break;
   }
 
   // ---- epilogue: lane holds column n0 + l % 32, rows 32 mt + acc_row(i, l) ----
