@@ -886,27 +886,30 @@ __global__ __launch_bounds__(256) void reduce_norm_kernel(const LinParams p) {
 // per CU (an L1 keeps ~84 L2 reads of 128 bytes in flight, ~40 GB/s): what matters is
 // spreading W evenly over all CUs.  A workgroup owns 8 output columns and all of K.
 // Thread t takes column n0 + t%8, half (t/8)%2 of each 16-wide k step, and steps
-// t/16, t/16 + 16, ...: in the packed layout each 16-thread group reads two contiguous
-// 128-byte pieces per step.  Each thread accumulates in k order in fp32; the 32 threads
-// of a column are combined by an xor-shuffle tree (within a wave) and then in wave
-// order through LDS -- deterministic.  Loads are issued U steps at a time ahead of their
-// use (clamped to the last step: every load is in bounds and unconditional, and a clamped
-// step is multiplied in with a zero weight).  U (3 or 4) is picked per call from the steps
-// per thread, T = ceil(K / 16 / 16): fewest load rounds, then fewest clamped steps -- at
-// the Mamba-130M shapes (T = 3 and 6) U = 3 wastes none where U = 4 wasted one or two per
-// round (130M decode 0.370-0.382 -> 0.364 ms per step; U = 2, 6, 8 measured 0.40, 0.39,
-// 0.42 ms).  The input
+// t/16, t/16 + SG, ... (SG = NT / 16 step groups): in the packed layout each 16-thread
+// group reads two contiguous 128-byte pieces per step.  Each thread accumulates in k
+// order in fp32; the NT / 8 threads of a column are combined by an xor-shuffle tree
+// (within a wave) and then in wave order through LDS -- deterministic.  Loads are issued
+// U steps at a time ahead of their use (clamped to the last step: every load is in bounds
+// and unconditional, and a clamped step is multiplied in with a zero weight).  The
+// workgroup size NT (256, 512 or 1024) gives each thread at most 4 steps, so one load
+// round covers K (a dependent memory round trip per further round is what this
+// latency-bound kernel pays for), and U (3 or 4) is then picked from the steps per thread:
+// fewest rounds, then fewest clamped steps.  Measured at the Mamba-130M decode (K = 768
+// and 1536): U = 3 instead of 4 wastes no step (0.370-0.382 -> 0.364 ms per step; U = 2,
+// 6, 8 measured 0.40, 0.39, 0.42 ms), and 512 threads for K = 1536 take x_proj and
+// out_proj from two load rounds to one (0.355 -> 0.337 ms per step).  The input
 // RMSNorm (NORM) is computed by wave 0 in add_rmsnorm_vec_kernel's order and applied as
 // each x chunk is loaded, as in linear_kernel.  Epilogues as the split-K reduce.
 constexpr int kGvCols = 8;
-constexpr int kGvThreads = 256;
 constexpr int kGvMaxM = 4;
 
-template <int DT, int MM, int EPI, bool NORM, int U>
-__global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
+template <int DT, int MM, int EPI, bool NORM, int U, int NT>
+__global__ __launch_bounds__(NT) void gemv_kernel(const LinParams p) {
+  constexpr int SG = NT / 16;  // step groups: thread t walks steps t/16, t/16 + SG, ...
   using T = typename Ty<DT>::T;
   using V8 = typename Ty<DT>::V8;
-  __shared__ float s_red[kGvThreads / 64][MM][kGvCols];
+  __shared__ float s_red[NT / 64][MM][kGvCols];
   __shared__ float s_inv[MM];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -922,7 +925,7 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
   for (int m = 0; m < MM; ++m)
     xr[m] = static_cast<const T*>(p.x) + (m < p.M ? m : 0) * p.ldx + 8 * hk;
 
-  // Load group at steps sb, sb + 16, ... (clamped to the last step; steps past the end
+  // Load group at steps sb, sb + SG, ... (clamped to the last step; steps past the end
   // count with a zero weight when consumed).
   const int64_t s_last = nsteps - 1;
   u32x4 wv[U], nv[U];
@@ -930,7 +933,7 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
   auto load = [&](int64_t sb) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t st = sb + 16 * u < nsteps ? sb + 16 * u : s_last;
+      const int64_t st = sb + SG * u < nsteps ? sb + SG * u : s_last;
       wv[u] = wb[st * 64];
 #pragma unroll
       for (int m = 0; m < MM; ++m) xv[u][m] = *reinterpret_cast<const V8*>(xr[m] + st * kStepK);
@@ -967,7 +970,7 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const u32x4 zero = {0u, 0u, 0u, 0u};
-      const V8 w8 = __builtin_bit_cast(V8, sb + 16 * u < nsteps ? wv[u] : zero);
+      const V8 w8 = __builtin_bit_cast(V8, sb + SG * u < nsteps ? wv[u] : zero);
 #pragma unroll
       for (int m = 0; m < MM; ++m) {
 #pragma unroll
@@ -979,11 +982,11 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
         }
       }
     }
-    sb += 16 * U;
+    sb += SG * U;
     if (sb >= nsteps) break;
     load(sb);
   }
-  // column sums: lanes j, j+8, ..., j+56 of a wave, then the 4 waves in order
+  // column sums: lanes j, j+8, ..., j+56 of a wave, then the NT / 64 waves in order
 #pragma unroll
   for (int m = 0; m < MM; ++m) {
 #pragma unroll
@@ -996,39 +999,57 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const LinParams p) {
     const int64_t nn = static_cast<int64_t>(blockIdx.x) * kGvCols + jj;
     float v = s_red[0][m][jj];
 #pragma unroll
-    for (int w = 1; w < kGvThreads / 64; ++w) v += s_red[w][m][jj];
+    for (int w = 1; w < NT / 64; ++w) v += s_red[w][m][jj];
     if (m < p.M && nn < p.N) epilogue<DT, EPI>(p, m, nn, v);
   }
 }
 
-template <int DT, int MM, bool NORM, int U>
+template <int DT, int MM, bool NORM, int U, int NT>
 void launch_gemv_u(const LinParams& p, int32_t epi, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(ceil_div(p.N, kGvCols)));
   switch (epi) {
     case MM_LIN_STORE:
-      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_STORE, NORM, U>), grid, dim3(kGvThreads), 0, s, p);
+      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_STORE, NORM, U, NT>), grid, dim3(NT), 0, s, p);
       break;
     case MM_LIN_RESID:
-      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_RESID, NORM, U>), grid, dim3(kGvThreads), 0, s, p);
+      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_RESID, NORM, U, NT>), grid, dim3(NT), 0, s, p);
       break;
     default:
-      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_CONV, NORM, U>), grid, dim3(kGvThreads), 0, s, p);
+      hipLaunchKernelGGL((gemv_kernel<DT, MM, MM_LIN_CONV, NORM, U, NT>), grid, dim3(NT), 0, s, p);
       break;
   }
 }
 
+// Threads per workgroup: enough 16-thread step groups that each thread has at most 4 steps
+// (one load round), up to 1024.
+inline int gemv_threads(int64_t K) {
+  const int64_t nsteps = K / kStepK;
+  int nt = 256;
+  while (nt < 1024 && ceil_div(nsteps, nt / 16) > 4) nt *= 2;
+  return nt;
+}
+
 // Steps loaded per round (see gemv_kernel): fewest rounds, then fewest clamped steps.
-inline int gemv_group(int64_t K) {
-  const int64_t t = ceil_div(K / kStepK, 16);  // steps per thread
+inline int gemv_group(int64_t K, int nt) {
+  const int64_t t = ceil_div(K / kStepK, nt / 16);  // steps per thread
   const int64_t r3 = ceil_div(t, 3), r4 = ceil_div(t, 4);
   if (r4 < r3) return 4;
   return (r3 * 3 - t) < (r4 * 4 - t) ? 3 : 4;
 }
 
+template <int DT, int MM, bool NORM, int NT>
+void launch_gemv_n(const LinParams& p, int32_t epi, hipStream_t s) {
+  if (gemv_group(p.K, NT) == 3) launch_gemv_u<DT, MM, NORM, 3, NT>(p, epi, s);
+  else launch_gemv_u<DT, MM, NORM, 4, NT>(p, epi, s);
+}
+
 template <int DT, int MM, bool NORM>
 void launch_gemv_e(const LinParams& p, int32_t epi, hipStream_t s) {
-  if (gemv_group(p.K) == 3) launch_gemv_u<DT, MM, NORM, 3>(p, epi, s);
-  else launch_gemv_u<DT, MM, NORM, 4>(p, epi, s);
+  switch (gemv_threads(p.K)) {
+    case 256: launch_gemv_n<DT, MM, NORM, 256>(p, epi, s); break;
+    case 512: launch_gemv_n<DT, MM, NORM, 512>(p, epi, s); break;
+    default: launch_gemv_n<DT, MM, NORM, 1024>(p, epi, s); break;
+  }
 }
 
 template <int DT>
