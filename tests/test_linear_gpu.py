@@ -33,12 +33,16 @@ def _check(got, ref, dtype, what):
 # (20, 128, 8200) give each wave two column tiles.  > 512 column tiles run the shared-X
 # kernel: (37, 256, 20000) with 4 waves and a ragged last tile, (64, 2560, 50280) and
 # (1, 768, 50280) (130M head at batch 1: one 32-row MFMA tile, X staged by half the
-# waves) with 8.
+# waves) with 8.  M <= 4 runs the GEMV, whose workgroup size and load group follow K:
+# (1, 768, 3072) 256 threads, groups of 3; (1, 1536, 80) 512, 3; (1, 1024, 136) 256, 4;
+# (2, 2560, 200) 1024, 3; (3, 5120, 72) 1024 threads, two rounds of 3 with one clamped
+# step; (4, 320, 40) 256 threads, one group of 3 with one clamped step; (1, 4096, 64) 1024, 4.
 @pytest.mark.parametrize("M,K,N", [(64, 2560, 10240), (64, 5120, 2560), (64, 5120, 192),
                                    (1, 768, 3072), (1, 1536, 80), (37, 1536, 100), (33, 256, 50),
                                    (37, 4096, 100), (32, 64, 33), (64, 2560, 50280), (5, 64, 7),
                                    (64, 64, 4096), (1, 768, 50280), (37, 256, 20000),
-                                   (20, 128, 8200)])
+                                   (20, 128, 8200), (1, 1024, 136), (2, 2560, 200), (3, 5120, 72),
+                                   (4, 320, 40), (1, 4096, 64)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_decode_linear(dev, M, K, N, dtype):
     from mamba_metal_amd.linear import decode_linear

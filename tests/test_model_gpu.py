@@ -303,6 +303,29 @@ def test_batched_decode_matches_oracle(dev, dtype, batch, tol):
         assert_close(gl[s].cpu().numpy(), ref_logits[s].numpy(), tol, tol, f"batch {batch} step {s}")
 
 
+@pytest.mark.parametrize("batch", [1, 3])
+def test_wide_gemv_decode_matches_oracle(dev, batch):
+    """2.8B width (d_model 2560, dt_rank 160; 2 layers), fp16, batch 1 and 3: the decode
+    step's GEMVs run 1024-thread workgroups (in_proj K = 2560 with the input norm and conv
+    window, x_proj and out_proj + residual K = 5120 in two load rounds).  Teacher-forced
+    logits of 4 steps against the float64 oracle."""
+    model, cfg = make_model(dev, dtype=torch.float16, seed=23, d_model=2560, n_layer=2,
+                            vocab_size=2048, dt_rank=160)
+    ref = ref_of(model, cfg)
+    rng = np.random.default_rng(23 + batch)
+    ids = torch.as_tensor(rng.integers(0, cfg.vocab_size, (batch, 12)), device=dev)
+    teacher = rng.integers(0, cfg.vocab_size, (batch, 4))
+    _, ref_logits = ref.generate_fast_ids(ids.cpu().numpy(), 4, teacher=teacher)
+    with torch.inference_mode():
+        lg, convs, ssms = model.prefill(ids, last_only=True)
+        gl = [lg[:, -1].float()]
+        for s in range(3):
+            lg, convs, ssms = model.step(torch.as_tensor(teacher[:, s:s + 1], device=dev), convs, ssms)
+            gl.append(lg[:, 0].float())
+    for s in range(4):
+        assert_close(gl[s].cpu().numpy(), ref_logits[s].numpy(), 2e-2, 2e-2, f"batch {batch} step {s}")
+
+
 def test_load_mamba_hf_roundtrip(dev, tmp_path):
     import json
 
