@@ -683,8 +683,20 @@ __global__ __launch_bounds__(NW * 64, 1) void share_kernel(const LinParams p) {
   load(s1, cbeg + 1);
   // Whole rounds while all three prefetches stay in range, then the last 1-4 chunks
   // straight-line: the round's prefetches of c + 3 and c + 4 would otherwise re-read
-  // the last chunk up to four more times.
+  // the last chunk up to four more times.  The conv epilogue keeps the plain loop: with
+  // its registers live the peeled tail would spill.
   int64_t c = cbeg;
+  if constexpr (EPI == MM_LIN_CONV) {
+    for (; c < nchunks; c += 3) {
+      load(s2, c + 2);
+      compute(s0, c, 0);
+      load(s0, c + 3);
+      compute(s1, c + 1, 1);
+      load(s1, c + 4);
+      compute(s2, c + 2, 2);
+    }
+    c = nchunks;  // nothing left for the tail below
+  }
   for (; c + 4 < nchunks; c += 3) {
     load(s2, c + 2);
     compute(s0, c, 0);
@@ -892,9 +904,10 @@ __global__ __launch_bounds__(256) void reduce_norm_kernel(const LinParams p) {
 // (within a wave) and then in wave order through LDS -- deterministic.  Loads are issued
 // U steps at a time ahead of their use (clamped to the last step: every load is in bounds
 // and unconditional, and a clamped step is multiplied in with a zero weight).  The
-// workgroup size NT (256, 512 or 1024) gives each thread at most 4 steps, so one load
-// round covers K (a dependent memory round trip per further round is what this
-// latency-bound kernel pays for), and U (3 or 4) is then picked from the steps per thread:
+// workgroup size NT (256, 512 or 1024, at most 1024 / rows) gives each thread at most 4
+// steps, so one load round covers K (a dependent memory round trip per further round is
+// what this latency-bound kernel pays for), and U (3 or 4) is then picked from the steps
+// per thread:
 // fewest rounds, then fewest clamped steps.  Measured at the Mamba-130M decode (K = 768
 // and 1536): U = 3 instead of 4 wastes no step (0.370-0.382 -> 0.364 ms per step; U = 2,
 // 6, 8 measured 0.40, 0.39, 0.42 ms), and 512 threads for K = 1536 take x_proj and
@@ -1021,11 +1034,13 @@ void launch_gemv_u(const LinParams& p, int32_t epi, hipStream_t s) {
 }
 
 // Threads per workgroup: enough 16-thread step groups that each thread has at most 4 steps
-// (one load round), up to 1024.
-inline int gemv_threads(int64_t K) {
+// (one load round), up to 1024 / MM -- with more rows the per-thread registers (MM x-row
+// vectors per step, the input-norm operands) no longer fit the smaller register share of a
+// larger workgroup and would spill.
+inline int gemv_threads(int64_t K, int mm) {
   const int64_t nsteps = K / kStepK;
   int nt = 256;
-  while (nt < 1024 && ceil_div(nsteps, nt / 16) > 4) nt *= 2;
+  while (nt < 1024 / mm && ceil_div(nsteps, nt / 16) > 4) nt *= 2;
   return nt;
 }
 
@@ -1045,11 +1060,14 @@ void launch_gemv_n(const LinParams& p, int32_t epi, hipStream_t s) {
 
 template <int DT, int MM, bool NORM>
 void launch_gemv_e(const LinParams& p, int32_t epi, hipStream_t s) {
-  switch (gemv_threads(p.K)) {
-    case 256: launch_gemv_n<DT, MM, NORM, 256>(p, epi, s); break;
-    case 512: launch_gemv_n<DT, MM, NORM, 512>(p, epi, s); break;
-    default: launch_gemv_n<DT, MM, NORM, 1024>(p, epi, s); break;
+  const int nt = gemv_threads(p.K, MM);
+  if constexpr (MM == 1) {
+    if (nt == 1024) return launch_gemv_n<DT, MM, NORM, 1024>(p, epi, s);
   }
+  if constexpr (MM <= 2) {
+    if (nt == 512) return launch_gemv_n<DT, MM, NORM, 512>(p, epi, s);
+  }
+  launch_gemv_n<DT, MM, NORM, 256>(p, epi, s);
 }
 
 template <int DT>
