@@ -218,22 +218,34 @@ __device__ __forceinline__ float row_sumsq(const typename Ty<DT>::T* r, int nch,
 // 8*(i/4) + 4*(l/32) + i%4, column l%32.
 __device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
+// LDS of one linear_kernel workgroup: a per-wave slot that holds the X chunk during the
+// K loop and the wave's partial tiles afterwards.
+template <int KSW, int MT, int NT, int EPI>
+struct LinLds {
+  static constexpr int kNacc = MT * NT * 16;  // accumulator floats per lane
+  static constexpr int kWave = kXLds > kNacc * 64 * 4 ? kXLds : kNacc * 64 * 4;
+  static constexpr int kBytes = (EPI == kPartial ? 1 : KSW) * kWave;
+};
+
+// The body of linear_kernel for column block t (TN = NT * 32 columns from t * TN) and K
+// split ks, on the workgroup's LDS block smem (LinLds bytes).  kZStore is the STORE
+// epilogue of the z half of in_proj (columns from n_conv on, stored to y[m, n - n_conv]).
+constexpr int kZStore = 5;
+
 template <int DT, int KSW, int MT, int NT, int EPI, bool NORM = false, bool XP = false>
-__global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
+__device__ __forceinline__ void linear_body(const LinParams& p, const int64_t t, const int ks,
+                                            char* const smem) {
   using T = typename Ty<DT>::T;
   using V8 = typename Ty<DT>::V8;
   static_assert(!NORM || MT == 1, "the input RMSNorm covers rows 0..7 of one m-tile");
   static_assert(!XP || (EPI == MM_LIN_CONV && KSW == 4 && !NORM), "x_proj rides the 4-wave conv epilogue");
   constexpr int XI = MT * 4;                 // X load instructions per chunk (8 rows each)
   constexpr int NACC = MT * NT * 16;         // accumulator floats per lane
-  constexpr int kWaveLds = kXLds > NACC * 64 * 4 ? kXLds : NACC * 64 * 4;
+  constexpr int kWaveLds = LinLds<KSW, MT, NT, EPI>::kWave;
   constexpr int TN = NT * kTileN;            // columns per workgroup
-  __shared__ __align__(16) char smem[(EPI == kPartial ? 1 : KSW) * kWaveLds];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   char* const xs = smem + (EPI == kPartial ? 0 : wave * kWaveLds);
-  const int64_t t = blockIdx.x;
-  const int ks = blockIdx.y;
   const int64_t n0 = t * TN;
   const int64_t nsteps = p.K / kStepK;
   const int64_t nchunks = p.K / kChunkK;
@@ -445,10 +457,11 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
       ms[u] = row;
       ns[u] = n0 + col;
     }
-    if constexpr (EPI == MM_LIN_STORE) {
+    if constexpr (EPI == MM_LIN_STORE || EPI == kZStore) {
+      const int64_t c0 = EPI == kZStore ? p.n_conv : 0;
 #pragma unroll
       for (int u = 0; u < EPT; ++u)
-        if (ms[u] < p.M && ns[u] < p.N) st<DT>(p.y, ms[u] * p.ldy + ns[u], vals[u]);
+        if (ms[u] < p.M && ns[u] < p.N) st<DT>(p.y, ms[u] * p.ldy + ns[u] - c0, vals[u]);
     } else if constexpr (EPI == MM_LIN_RESID) {
       T* const rb = static_cast<T*>(p.resid);
       T old[EPT];
@@ -532,6 +545,31 @@ __global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
       }
     }
   }
+}
+
+template <int DT, int KSW, int MT, int NT, int EPI, bool NORM = false, bool XP = false>
+__global__ __launch_bounds__(KSW * 64) void linear_kernel(const LinParams p) {
+  __shared__ __align__(16) char smem[LinLds<KSW, MT, NT, EPI>::kBytes];
+  linear_body<DT, KSW, MT, NT, EPI, NORM, XP>(p, blockIdx.x, blockIdx.y, smem);
+}
+
+// in_proj + conv window + x_proj partials with the two halves on different column
+// blocks: the conv half (n < n_conv), whose workgroups also run the conv step and the
+// x_proj product after the K loop, on NTC = 1 tile (32 columns) per workgroup; the z half
+// on NTZ = 2 tiles.  With the 2-tile blocks everywhere the conv-half workgroups (same
+// weight and X bytes as the z half, plus the epilogue) set the kernel's time; on 1-tile
+// blocks their K loop moves a third fewer bytes and the grid covers more CUs (Mamba-2.8B:
+// 160 + 80 workgroups instead of 80 + 80).  Workgroups [0, conv_wgs) take the conv half.
+template <int DT, int MT, int NTC, int NTZ>
+__global__ __launch_bounds__(256) void in_proj_split_kernel(const LinParams p, int64_t conv_wgs) {
+  constexpr int kC = LinLds<4, MT, NTC, MM_LIN_CONV>::kBytes;
+  constexpr int kZ = LinLds<4, MT, NTZ, kZStore>::kBytes;
+  __shared__ __align__(16) char smem[kC > kZ ? kC : kZ];
+  const int64_t b = blockIdx.x;
+  if (b < conv_wgs)
+    linear_body<DT, 4, MT, NTC, MM_LIN_CONV, false, true>(p, b, 0, smem);
+  else
+    linear_body<DT, 4, MT, NTZ, kZStore>(p, p.n_conv / (NTZ * kTileN) + (b - conv_wgs), 0, smem);
 }
 
 // x_proj planes of mm_decode_in_proj_xproj summed: y[m, n] = round(sum_p part[p][m][n]).
@@ -1160,9 +1198,28 @@ void launch_main(const LinParams& p, int32_t epi, const Plan& pl, dim3 grid, hip
 
 // in_proj + conv window + x_proj partials (then xp_reduce_kernel): the 4-wave linear_kernel
 // shapes only (see xp_fusable).
+// Whether in_proj_split_kernel runs the fused call: 2-tile column blocks in the plan, z
+// blocks aligned to n_conv, and 1-tile conv blocks + 2-tile z blocks within one
+// workgroup per CU.
+inline bool xp_split(const LinParams& p, const Plan& pl) {
+  const int64_t wgs = p.n_conv / kTileN + ceil_div(p.N - p.n_conv, 2 * kTileN);
+  return pl.nt == 2 && p.n_conv % (2 * kTileN) == 0 && wgs <= num_cus();
+}
+
 template <int DT>
 void launch_main_xp(const LinParams& p, const Plan& pl, dim3 grid, hipStream_t s) {
   const dim3 block(4 * 64);
+  if (xp_split(p, pl)) {
+    const int64_t conv_wgs = p.n_conv / kTileN;
+    const dim3 sgrid(static_cast<unsigned>(conv_wgs + ceil_div(p.N - p.n_conv, 2 * kTileN)));
+    if (p.M > 32)
+      hipLaunchKernelGGL((in_proj_split_kernel<DT, 2, 1, 2>), sgrid, block, 0, s, p, conv_wgs);
+    else
+      hipLaunchKernelGGL((in_proj_split_kernel<DT, 1, 1, 2>), sgrid, block, 0, s, p, conv_wgs);
+    const dim3 rgrid(static_cast<unsigned>(ceil_div(p.M * ceil_div(p.xp_n, 4), 16)));
+    hipLaunchKernelGGL((xp_reduce_kernel<DT>), rgrid, dim3(256), 0, s, p, conv_wgs);
+    return;
+  }
   if (p.M > 32 && pl.nt == 2)
     hipLaunchKernelGGL((linear_kernel<DT, 4, 2, 2, MM_LIN_CONV, false, true>), grid, block, 0, s, p);
   else if (p.M > 32)
@@ -1189,9 +1246,12 @@ inline bool xp_fusable(int64_t M, int64_t N, int64_t K, int64_t n_conv, int64_t 
          n_conv % kChunkK == 0;
 }
 
+// One fp32 (M, xp_n) plane per conv-half workgroup; sized for 1-tile conv blocks (the
+// split kernel's, the larger count) whatever the device, so the size does not depend on it.
 inline size_t xp_workspace(int64_t M, int64_t N, int64_t K, int64_t n_conv, int64_t xp_n) {
-  const Plan pl = plan(N, K);
-  return static_cast<size_t>(n_conv / (kTileN * pl.nt)) * static_cast<size_t>(M * xp_n) * 4;
+  (void)N;
+  (void)K;
+  return static_cast<size_t>(n_conv / kTileN) * static_cast<size_t>(M * xp_n) * 4;
 }
 
 struct XpArgs {

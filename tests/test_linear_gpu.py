@@ -182,13 +182,15 @@ def test_decode_in_proj_conv(dev, K, di, M, dtype):
 
 # in_proj + conv window + x_proj (mm_decode_in_proj_xproj).  Fused -- x_proj products
 # taken in in_proj's conv epilogue, fp32 partial planes summed by one kernel: 2.8B shape
-# (two 32-column tiles per wave, 80 planes of 64 conv columns), 130M at batch 16 (one
-# m-tile) and 33 (two), an x_proj of 256 columns (every wave two tiles).  Falling back to
+# at batch 64 and 16 and the 1.4B shape (the split kernel: 32-column conv blocks, one
+# plane each, and 64-column z blocks), 130M at batch 16 (one m-tile) and 33 (two), an
+# x_proj of 256 columns (every wave two tiles).  Falling back to
 # two GEMMs: batch 3 (GEMV in_proj), an x_proj width that is not a multiple of 4, the
 # input RMSNorm.  The in_proj outputs must equal decode_in_proj_conv's bit for bit; x_dbl
 # is checked against the fp32 product of the returned conv outputs.
 @pytest.mark.parametrize("M,K,di,nx,norm,fused", [
-    (64, 2560, 5120, 192, False, True), (16, 768, 1536, 80, False, True),
+    (64, 2560, 5120, 192, False, True), (16, 2560, 5120, 192, False, True),
+    (64, 2048, 4096, 160, False, True), (16, 768, 1536, 80, False, True),
     (33, 768, 1536, 80, False, True), (64, 512, 640, 256, False, True),
     (3, 768, 1536, 80, False, False), (8, 768, 1536, 50, False, False),
     (8, 768, 1536, 80, True, False)])
@@ -214,11 +216,10 @@ def test_decode_in_proj_conv_xproj(dev, M, K, di, nx, norm, fused, dtype):
     _check(x_dbl, _ref(x_conv, wx), dtype, "x_proj")
     _, _, x_dbl2 = decode_in_proj_conv_xproj(x, w, st_c, cw, cb, wx, x_norm=fold)
     assert torch.equal(x_dbl2, x_dbl)                      # fixed summation order
-    # the fused shapes size the workspace for (n_conv / tile width) fp32 planes of M x nx
+    # the fused shapes size the workspace for one fp32 plane of M x nx per 32 conv columns
     if fused:
-        tn = 64 if 2 * di >= 256 * 32 else 32
         ws = _lib.load().mm_decode_in_proj_xproj_workspace_size(M, 2 * di, K, di, nx)
-        assert ws >= (di // tn) * M * nx * 4
+        assert ws >= (di // 32) * M * nx * 4
 
 
 # Input RMSNorm folded into the operand load: the product must be bit-identical to the
