@@ -575,11 +575,12 @@ __global__ __launch_bounds__(256) void in_proj_split_kernel(const LinParams p, i
 // x_proj planes of mm_decode_in_proj_xproj summed: y[m, n] = round(sum_p part[p][m][n]).
 // A workgroup covers 16 four-column groups; its 16 thread slices each sum a contiguous
 // run of planes in order (all loads of a run issued together), then slice 0 adds the 16
-// run sums in order -- a fixed summation order, so results are reproducible.
-template <int DT>
+// run sums in order -- a fixed summation order, so results are reproducible.  kRun (8 or
+// 16, picked by the launcher) covers a slice's run in one round of loads up to 256
+// planes.
+template <int DT, int kRun>  // kRun: planes per thread slice and pass (loads in flight)
 __global__ __launch_bounds__(256) void xp_reduce_kernel(const LinParams p, int64_t nplanes) {
   __shared__ f32x4 s_sum[16][16];
-  constexpr int kRun = 8;  // planes per thread slice and pass (loads in flight)
   const int gq = threadIdx.x & 15, sl = threadIdx.x >> 4;
   const int64_t nq = (p.xp_n + 3) / 4;
   const int64_t q = static_cast<int64_t>(blockIdx.x) * 16 + gq;
@@ -1198,6 +1199,15 @@ void launch_main(const LinParams& p, int32_t epi, const Plan& pl, dim3 grid, hip
 
 // in_proj + conv window + x_proj partials (then xp_reduce_kernel): the 4-wave linear_kernel
 // shapes only (see xp_fusable).
+template <int DT>
+void launch_xp_reduce(const LinParams& p, int64_t nplanes, hipStream_t s) {
+  const dim3 rgrid(static_cast<unsigned>(ceil_div(p.M * ceil_div(p.xp_n, 4), 16)));
+  if (ceil_div(nplanes, 16) > 8)
+    hipLaunchKernelGGL((xp_reduce_kernel<DT, 16>), rgrid, dim3(256), 0, s, p, nplanes);
+  else
+    hipLaunchKernelGGL((xp_reduce_kernel<DT, 8>), rgrid, dim3(256), 0, s, p, nplanes);
+}
+
 // Whether in_proj_split_kernel runs the fused call: 2-tile column blocks in the plan, z
 // blocks aligned to n_conv, and 1-tile conv blocks + 2-tile z blocks within one
 // workgroup per CU.
@@ -1216,8 +1226,7 @@ void launch_main_xp(const LinParams& p, const Plan& pl, dim3 grid, hipStream_t s
       hipLaunchKernelGGL((in_proj_split_kernel<DT, 2, 1, 2>), sgrid, block, 0, s, p, conv_wgs);
     else
       hipLaunchKernelGGL((in_proj_split_kernel<DT, 1, 1, 2>), sgrid, block, 0, s, p, conv_wgs);
-    const dim3 rgrid(static_cast<unsigned>(ceil_div(p.M * ceil_div(p.xp_n, 4), 16)));
-    hipLaunchKernelGGL((xp_reduce_kernel<DT>), rgrid, dim3(256), 0, s, p, conv_wgs);
+    launch_xp_reduce<DT>(p, conv_wgs, s);
     return;
   }
   if (p.M > 32 && pl.nt == 2)
@@ -1228,9 +1237,7 @@ void launch_main_xp(const LinParams& p, const Plan& pl, dim3 grid, hipStream_t s
     hipLaunchKernelGGL((linear_kernel<DT, 4, 1, 2, MM_LIN_CONV, false, true>), grid, block, 0, s, p);
   else
     hipLaunchKernelGGL((linear_kernel<DT, 4, 1, 1, MM_LIN_CONV, false, true>), grid, block, 0, s, p);
-  const int64_t nplanes = p.n_conv / (kTileN * pl.nt);
-  const dim3 rgrid(static_cast<unsigned>(ceil_div(p.M * ceil_div(p.xp_n, 4), 16)));
-  hipLaunchKernelGGL((xp_reduce_kernel<DT>), rgrid, dim3(256), 0, s, p, nplanes);
+  launch_xp_reduce<DT>(p, p.n_conv / (kTileN * pl.nt), s);
 }
 
 // Whether mm_decode_in_proj_xproj folds x_proj into in_proj's conv epilogue: the call
