@@ -428,12 +428,12 @@ __global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_mfma_kernel(const F
   const T biasr = static_cast<const T*>(p.bias ? p.bias : p.x)[p.bias ? cc : 0];
   const float Dr = p.D ? p.D[cc] : 0.0f;
   const T* const zp = static_cast<const T*>(p.z ? p.z : p.x);
-  float4 hv[kMBB];
+  f32x4 hv[kMBB];  // state rows: read and written once per step (non-temporal)
   T xr[kMBB], zr[kMBB];
 #pragma unroll
   for (int bb = 0; bb < kMBB; ++bb) {
     const int64_t b = b0 + bb < p.batch ? b0 + bb : 0;
-    hv[bb] = *reinterpret_cast<const float4*>(p.h + (b * p.dim + cc) * kFusedNS + q * 4);
+    hv[bb] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p.h + (b * p.dim + cc) * kFusedNS + q * 4));
     xr[bb] = static_cast<const T*>(p.x)[b * p.xsb + cc];
     zr[bb] = zp[p.z ? b * p.zsb + cc : b * p.xsb + cc];
   }
@@ -466,7 +466,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_mfma_kernel(const F
     const float xv = Ty<DT>::f(xr[bb]);
     const float dtv = softplus_full(s_dt[wave][bb][cl] + bias);
     const float du = dtv * xv;
-    float hs[4] = {hv[bb].x, hv[bb].y, hv[bb].z, hv[bb].w};
+    float hs[4] = {hv[bb][0], hv[bb][1], hv[bb][2], hv[bb][3]};
     float yacc = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -474,7 +474,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void ssm_step_mfma_kernel(const F
       hs[k] = __builtin_fmaf(a, hs[k], du * s_B[bb][q * 4 + k]);
       yacc = __builtin_fmaf(hs[k], s_C[bb][q * 4 + k], yacc);
     }
-    if (cok) *reinterpret_cast<float4*>(hw + bb * p.dim * kFusedNS) = make_float4(hs[0], hs[1], hs[2], hs[3]);
+    if (cok) __builtin_nontemporal_store(f32x4{hs[0], hs[1], hs[2], hs[3]}, reinterpret_cast<f32x4*>(hw + bb * p.dim * kFusedNS));
     yacc += lane_xor(yacc, 1);
     yacc += lane_xor(yacc, 2);
     if (q == 0 && cok) {
