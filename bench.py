@@ -318,7 +318,7 @@ def cpu_baseline(batch, dim, dstate, seqlen, n_channels=5120):
 
 
 def decode_bench(name, cfg_kw, batch, prompt_len, n_decode, seed=0):
-    """Random-init model: parallel prefill, then n_decode greedy steps (HIP graph)."""
+    """Random-init model: parallel prefill, then n_decode greedy steps (HIP graph of 8 steps)."""
     import torch
 
     from mamba_metal_amd import GraphDecoder, MambaConfig, MambaModel, init_weights_
@@ -331,8 +331,8 @@ def decode_bench(name, cfg_kw, batch, prompt_len, n_decode, seed=0):
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     ids = torch.randint(0, cfg.vocab_size, (batch, prompt_len), generator=g, device=dev)
-    dec = GraphDecoder(model, batch, use_graph=True)
-    dec.start(ids)                           # warm-up prefill + graph capture
+    dec = GraphDecoder(model, batch, use_graph=True, steps_per_graph=8)
+    dec.start(ids)                           # warm-up prefill + graph capture (8 steps a replay)
     for _ in range(3):
         dec.step()
     torch.cuda.synchronize()

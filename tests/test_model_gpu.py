@@ -175,14 +175,16 @@ def test_greedy_ids_match_oracle_fp32(dev, small):
     assert np.array_equal(got, want.numpy())
 
 
-def test_graph_decoder_matches_eager(dev, small):
-    """HIP-graph replays == eager steps, replay after replay, with eager work between."""
+@pytest.mark.parametrize("k", [1, 4])
+def test_graph_decoder_matches_eager(dev, small, k):
+    """HIP-graph replays == eager steps, replay after replay, with eager work between; with
+    k steps per graph (k = 4: 11 steps take three replays, the last one partly used)."""
     from mamba_metal_amd import GraphDecoder, generate_fast_ids
 
     model, cfg, _ = small
     ids = torch.as_tensor(np.random.default_rng(5).integers(0, cfg.vocab_size, (4, 25)), device=dev)
     eager = generate_fast_ids(model, ids, 12).cpu().numpy()
-    dec = GraphDecoder(model, 4, use_graph=True)
+    dec = GraphDecoder(model, 4, use_graph=True, steps_per_graph=k)
     toks = [dec.start(ids).cpu().numpy()]
     for _ in range(11):
         toks.append(dec.step().cpu().numpy())
@@ -194,6 +196,9 @@ def test_graph_decoder_matches_eager(dev, small):
         toks.append(dec.step().cpu().numpy())
     assert np.array_equal(np.stack(toks, 1), eager)
     assert np.array_equal(generate_fast_ids(model, ids, 12, use_graph=True).cpu().numpy(), eager)
+    # 9 tokens: 8 steps after the first, one 8-step graph
+    assert np.array_equal(generate_fast_ids(model, ids, 9, use_graph=True).cpu().numpy(),
+                          eager[:, :9])
 
 
 @pytest.mark.parametrize("shape", ["130m", "2.8b-width"])
