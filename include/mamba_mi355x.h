@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 4
+#define MM_ABI_VERSION 5
 /* Largest d_state accepted: mamba_metal/selective_scan.py:9 (MAX_DSTATE = 64). */
 #define MM_MAX_DSTATE 64
 
@@ -326,6 +326,18 @@ size_t mm_decode_in_proj_xproj_workspace_size(int64_t M, int64_t N, int64_t K, i
                                               int64_t xp_n);
 int mm_decode_in_proj_xproj(const mm_linear_params* params, const void* xp_w_packed,
                             int64_t xp_n, void* xp_y, int64_t ld_xp, void* stream);
+
+/* LM head + greedy choice of one decode step -- replaces the tied head
+ * (mamba_model.py:78, logits = h @ E^T) followed by generate_fast's greedy
+ * `mx.argmax(logits[:, -1, :])` (generate.py:91-93): runs mm_decode_linear(params)
+ * (epilogue MM_LIN_STORE: the logits y are stored as there) and writes ids[m] = the
+ * column of the largest stored y[m, :] (lowest column on ties, a NaN beats every
+ * number: mm_argmax_rows's result on the stored logits).  For the wide N of a head the
+ * per-workgroup maxima are taken in the GEMM's epilogue and one small kernel picks
+ * among them; otherwise mm_argmax_rows runs on y.  ids int64 (M,), 8-byte aligned;
+ * params->workspace must hold mm_decode_head_argmax_workspace_size bytes. */
+size_t mm_decode_head_argmax_workspace_size(int64_t M, int64_t N, int64_t K);
+int mm_decode_head_argmax(const mm_linear_params* params, int64_t* ids, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Prefill projection GEMM for short K -- replaces the dt projection of the parallel

@@ -61,6 +61,7 @@ constexpr int kMaxM = 64;
 constexpr int kRowBytes = kChunkK * 2 + 16;  // padded LDS row of one X chunk
 constexpr int kXLds = kMaxM * kRowBytes;     // 9216 B per wave for the X chunk
 constexpr int kPartial = 4;                  // internal "epilogue": write fp32 partials
+constexpr int kStoreArgmax = 6;              // share_kernel: STORE + per-row argmax candidates
 constexpr int kShareTiles = 512;             // wider N runs the shared-X kernel
 constexpr int kNormInMaxM = 8;               // input RMSNorm: rows of X load instruction 0
 constexpr int kNormInMaxK = 4096;            // input RMSNorm: rows add_rmsnorm_vec_kernel takes
@@ -104,6 +105,10 @@ struct LinParams {
   int64_t M, N, K, ldx, ldy, ldr, ldc, ldn, n_conv;
   float eps, x_eps;
   int32_t ks;       // K splits across workgroups (grid.y)
+  // kStoreArgmax: per (workgroup, row) the best stored logit and its column,
+  // cand_v[blockIdx.x * M + m] / cand_i[...]
+  float* cand_v;
+  int32_t* cand_i;
 };
 
 struct Plan {
@@ -623,6 +628,61 @@ __global__ __launch_bounds__(256) void xp_reduce_kernel(const LinParams p, int64
 // scratch or LDS).  A buffer is rewritten three chunks after it was read, i.e. after
 // two more barriers, by which time every wave's reads of it have completed.  The
 // epilogue stores straight from the accumulators: lane l holds column n0 + l % 32.
+// a better than b for a greedy argmax: NaN first, then the larger value, then the lower
+// index (torch.argmax's conventions, as mm_argmax_rows).
+__device__ __forceinline__ bool arg_better(float av, int32_t ai, float bv, int32_t bi) {
+  const bool an = av != av, bn = bv != bv;
+  if (an != bn) return an;
+  if (!an && av != bv) return av > bv;
+  return ai < bi;
+}
+
+// Second pass of mm_decode_head_argmax: one workgroup per row picks among the nwg
+// workgroup candidates (in that order, so ties keep the lowest column).
+__global__ __launch_bounds__(256) void head_argmax_kernel(const float* __restrict__ cand_v,
+                                                          const int32_t* __restrict__ cand_i,
+                                                          int64_t nwg, int64_t M,
+                                                          int64_t* __restrict__ ids) {
+  __shared__ float s_v[4];
+  __shared__ int32_t s_i[4];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  float bv = -__builtin_inff();
+  int32_t bi = 0x7fffffff;
+  for (int64_t w = tid; w < nwg; w += 256) {
+    const float v = cand_v[w * M + r];
+    const int32_t i = cand_i[w * M + r];
+    if (arg_better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float ov = lane_xor(bv, off);
+    const int32_t oi = __float_as_int(lane_xor(__int_as_float(bi), off));
+    if (arg_better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if ((tid & 63) == 0) {
+    s_v[tid >> 6] = bv;
+    s_i[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    bv = s_v[0];
+    bi = s_i[0];
+    for (int w = 1; w < 4; ++w)
+      if (arg_better(s_v[w], s_i[w], bv, bi)) {
+        bv = s_v[w];
+        bi = s_i[w];
+      }
+    ids[r] = bi;
+  }
+}
+
 template <int XPW>
 struct ShareSlot {
   u32x4 w[kSteps];
@@ -778,7 +838,7 @@ __global__ __launch_bounds__(NW * 64, 1) void share_kernel(const LinParams p) {
         const int64_t m = 32 * mt + acc_row(i, lane);
         if (ncol && m < p.M) dst[m * p.N + n] = acc[mt][i];
       }
-  } else if constexpr (EPI == MM_LIN_STORE) {
+  } else if constexpr (EPI == MM_LIN_STORE || EPI == kStoreArgmax) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -786,6 +846,67 @@ __global__ __launch_bounds__(NW * 64, 1) void share_kernel(const LinParams p) {
         const int64_t m = 32 * mt + acc_row(i, lane);
         if (ncol && m < p.M) st<DT>(p.y, m * p.ldy + n, acc[mt][i]);
       }
+    if constexpr (EPI == kStoreArgmax) {
+      // Greedy argmax of the stored (rounded) logits, torch.argmax's order: NaN first,
+      // then the larger value, then the lower column.  Per m-tile each wave transposes its
+      // 32 x 32 tile through LDS (lane l holds rows acc_row(., l) of column l % 32); lane
+      // l then scans row l / 2, columns 16 (l % 2) .. + 15 in order, the two halves meet
+      // in one exchange, and the NW waves' row maxima are combined in wave order (lower
+      // columns first).  One candidate per row and workgroup goes to cand_v / cand_i;
+      // head_argmax_kernel picks among those.
+      __shared__ float s_t[NW][32][33];
+      __syncthreads();  // every wave is past its last MFMA read of xs
+      float* const cv = reinterpret_cast<float*>(&xs[0][0]);      // [NW][MT * 32]
+      int32_t* const ci = reinterpret_cast<int32_t*>(cv + NW * MT * 32);
+      const int r = lane >> 1, half = lane & 1;
+      const int64_t nw0 = n0;  // this wave's first column
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          s_t[wave][acc_row(i, lane)][lane & 31] =
+              ncol ? Ty<DT>::f(Ty<DT>::from(acc[mt][i])) : -__builtin_inff();
+        __builtin_amdgcn_wave_barrier();  // LDS is in order per wave: the reads see the writes
+        float bv = -__builtin_inff();
+        int32_t bi = 0x7fffffff;
+        if (32 * mt + r < p.M) {
+#pragma unroll
+          for (int c = 0; c < 16; ++c) {
+            const int col = 16 * half + c;
+            const float v = s_t[wave][r][col];
+            const bool in = nw0 + col < p.N;
+            const bool t = in && (bi == 0x7fffffff || v > bv || (v != v && bv == bv));
+            bv = t ? v : bv;
+            bi = t ? static_cast<int32_t>(nw0 + col) : bi;
+          }
+        }
+        const float ov = lane_xor(bv, 1);
+        const int32_t oi = __float_as_int(lane_xor(__int_as_float(bi), 1));
+        if (arg_better(ov, oi, bv, bi)) {
+          bv = ov;
+          bi = oi;
+        }
+        if (half == 0) {
+          cv[wave * MT * 32 + 32 * mt + r] = bv;
+          ci[wave * MT * 32 + 32 * mt + r] = bi;
+        }
+        __builtin_amdgcn_wave_barrier();  // the next m-tile rewrites s_t[wave]
+      }
+      __syncthreads();
+      if (threadIdx.x < MT * 32 && threadIdx.x < p.M) {
+        const int rr = threadIdx.x;
+        float bv = cv[rr];
+        int32_t bi = ci[rr];
+#pragma unroll
+        for (int w = 1; w < NW; ++w)
+          if (arg_better(cv[w * MT * 32 + rr], ci[w * MT * 32 + rr], bv, bi)) {
+            bv = cv[w * MT * 32 + rr];
+            bi = ci[w * MT * 32 + rr];
+          }
+        p.cand_v[static_cast<int64_t>(blockIdx.x) * p.M + rr] = bv;
+        p.cand_i[static_cast<int64_t>(blockIdx.x) * p.M + rr] = bi;
+      }
+    }
   } else if constexpr (EPI == MM_LIN_RESID) {
     T* const rb = static_cast<T*>(p.resid);
     T old[MT][16];
@@ -1281,6 +1402,9 @@ void launch_share_epi(const LinParams& p, int32_t epi, dim3 grid, hipStream_t s)
     case MM_LIN_RESID:
       hipLaunchKernelGGL((share_kernel<DT, NW, MT, MM_LIN_RESID>), grid, block, 0, s, p);
       break;
+    case kStoreArgmax:
+      hipLaunchKernelGGL((share_kernel<DT, NW, MT, kStoreArgmax>), grid, block, 0, s, p);
+      break;
     default:
       hipLaunchKernelGGL((share_kernel<DT, NW, MT, MM_LIN_CONV>), grid, block, 0, s, p);
       break;
@@ -1402,7 +1526,21 @@ namespace gemm {
 
 // mm_decode_linear; with xp (only when xp_fusable) in_proj's conv epilogue also runs
 // x_proj on the conv outputs.
-static int decode_linear_core(const mm_linear_params* prm, void* stream, const XpArgs* xp) {
+// Whether mm_decode_head_argmax takes the argmax candidates in the GEMM's epilogue: the
+// shared-X kernel without a K split (the LM head's wide N) and a plain store.
+inline bool head_fusable(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || M > kMaxM || N < 1 || K < 1 || K % kChunkK != 0 || use_gemv(M, N)) return false;
+  const Plan pl = plan(N, K);
+  return pl.nw > 0 && pl.ks == 1;
+}
+
+inline size_t head_cand_bytes(int64_t M, int64_t N, int64_t K) {
+  const Plan pl = plan(N, K);
+  return static_cast<size_t>(ceil_div(N, kTileN * pl.nw)) * static_cast<size_t>(M) * 8;
+}
+
+static int decode_linear_core(const mm_linear_params* prm, void* stream, const XpArgs* xp,
+                              int64_t* argmax_ids = nullptr) {
   if (!prm) return fail(MM_ERR_NULL_POINTER, "params is NULL");
   const mm_linear_params& q = *prm;
   if (!q.x || !q.w_packed) return fail(MM_ERR_NULL_POINTER, "x and w_packed are required");
@@ -1445,8 +1583,11 @@ static int decode_linear_core(const mm_linear_params* prm, void* stream, const X
   }
   if (q.M == 0 || q.N == 0) return MM_OK;
   const Plan pl = plan(q.N, q.K);
-  const size_t need = xp ? xp_workspace(q.M, q.N, q.K, q.n_conv, xp->n)
-                         : mm_decode_linear_workspace_size(q.M, q.N, q.K);
+  const bool fuse_argmax = argmax_ids != nullptr && q.epilogue == MM_LIN_STORE && !q.x_norm_w &&
+                           head_fusable(q.M, q.N, q.K);
+  size_t need = xp ? xp_workspace(q.M, q.N, q.K, q.n_conv, xp->n)
+                   : mm_decode_linear_workspace_size(q.M, q.N, q.K);
+  if (fuse_argmax) need = std::max(need, head_cand_bytes(q.M, q.N, q.K));
   if (need > 0) {
     if (!q.workspace || q.workspace_bytes < need)
       return fail(MM_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need,
@@ -1484,6 +1625,10 @@ static int decode_linear_core(const mm_linear_params* prm, void* stream, const X
   p.xp_n = xp ? xp->n : 0;
   p.xp_nsteps = xp ? q.n_conv / kStepK : 0;
   p.ld_xp = xp ? xp->ld : 0;
+  p.cand_v = fuse_argmax ? static_cast<float*>(q.workspace) : nullptr;
+  p.cand_i = fuse_argmax ? reinterpret_cast<int32_t*>(static_cast<float*>(q.workspace) +
+                                                      ceil_div(q.N, kTileN * pl.nw) * q.M)
+                         : nullptr;
   const dim3 grid(static_cast<unsigned>(ceil_div(q.N, kTileN * (pl.nw > 0 ? pl.nw : pl.nt))),
                   static_cast<unsigned>(pl.ks));
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1495,6 +1640,13 @@ static int decode_linear_core(const mm_linear_params* prm, void* stream, const X
     if (q.dtype == MM_F16) launch_main_xp<MM_F16>(p, pl, grid, s);
     else launch_main_xp<MM_BF16>(p, pl, grid, s);
     return check_launch("decode_in_proj_xproj");
+  }
+  if (fuse_argmax) {
+    if (q.dtype == MM_F16) launch_share<MM_F16>(p, kStoreArgmax, pl, grid, s);
+    else launch_share<MM_BF16>(p, kStoreArgmax, pl, grid, s);
+    hipLaunchKernelGGL(head_argmax_kernel, dim3(static_cast<unsigned>(q.M)), dim3(256), 0, s,
+                       p.cand_v, p.cand_i, static_cast<int64_t>(grid.x), q.M, argmax_ids);
+    return check_launch("decode_head_argmax");
   }
   if (use_gemv(q.M, q.N)) {
     if (q.dtype == MM_F16) launch_gemv<MM_F16>(p, epi, s);
@@ -1535,6 +1687,29 @@ extern "C" {
 int mm_decode_linear(const mm_linear_params* prm, void* stream) {
   mm::clear_error();
   return mm::gemm::decode_linear_core(prm, stream, nullptr);
+}
+
+size_t mm_decode_head_argmax_workspace_size(int64_t M, int64_t N, int64_t K) {
+  using namespace mm::gemm;
+  const size_t lin = mm_decode_linear_workspace_size(M, N, K);
+  return head_fusable(M, N, K) ? std::max(lin, head_cand_bytes(M, N, K)) : lin;
+}
+
+int mm_decode_head_argmax(const mm_linear_params* prm, int64_t* ids, void* stream) {
+  using namespace mm;
+  using namespace mm::gemm;
+  clear_error();
+  if (!prm) return fail(MM_ERR_NULL_POINTER, "params is NULL");
+  if (!ids) return fail(MM_ERR_NULL_POINTER, "ids is required");
+  if (prm->epilogue != MM_LIN_STORE) return fail(MM_ERR_SHAPE, "the head takes the MM_LIN_STORE epilogue");
+  if (prm->N > 0x3fffffffLL) return fail(MM_ERR_SHAPE, "N too large for 32-bit column indices");
+  if (prm->ldy < prm->N) return fail(MM_ERR_LAYOUT, "ldy < N");
+  if (!aligned(ids, 8)) return fail(MM_ERR_LAYOUT, "ids must be 8-byte aligned");
+  if (!prm->x_norm_w && head_fusable(prm->M, prm->N, prm->K))
+    return decode_linear_core(prm, stream, nullptr, ids);
+  const int st = decode_linear_core(prm, stream, nullptr);
+  if (st != MM_OK || prm->M == 0 || prm->N == 0) return st;
+  return mm_argmax_rows(prm->y, prm->M, prm->N, prm->ldy, prm->dtype, ids, stream);
 }
 
 size_t mm_decode_in_proj_xproj_workspace_size(int64_t M, int64_t N, int64_t K, int64_t n_conv,

@@ -185,10 +185,9 @@ class GraphDecoder:
 
     def _step_into(self, src, dst):
         """One decode step on input ids ``src``; its greedy ids go to ``dst`` (which may be
-        ``src``: the embedding reads it before the argmax writes)."""
-        logits, _, _ = self.model.step(src.view(-1, 1), self.convs, self.ssms, inplace=True)
-        row = logits[:, 0, :]
-        argmax_rows(row if row.stride(-1) == 1 else row.contiguous(), out=dst)
+        ``src``: the embedding reads it before the argmax writes).  The head and the
+        argmax run as one call (``MambaModel.step_greedy``)."""
+        self.model.step_greedy(src.view(-1, 1), self.convs, self.ssms, dst)
         return dst
 
     def _eager_step(self):

@@ -7,6 +7,7 @@ wrappers run them on libmamba_mi355x's MFMA kernel, with the decode step's
 neighbouring element-wise ops folded into its epilogue:
 
 * ``decode_linear(x, w)``                  y = x @ w.T
+* ``decode_head_argmax(x, w, ids)``        y = x @ w.T and ids = argmax over each row of y
 * ``decode_linear_resid_(resid, x, w)``    resid += round(x @ w.T)   (out_proj + residual add)
 * ``decode_linear_resid_norm_(resid, x, w, norm_w, eps)``
       the same, then returns RMSNorm(resid) * norm_w (the next layer's input)
@@ -159,6 +160,30 @@ def decode_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = N
         raise ValueError("out must be (M, N) with x's dtype and unit inner stride")
     prm.y, prm.ldy = out.data_ptr(), out.stride(0)
     _call(prm, dev)
+    return out
+
+
+def decode_head_argmax(x: torch.Tensor, w: torch.Tensor, ids: torch.Tensor,
+                       out: torch.Tensor | None = None):
+    """logits (M, N) = x @ w.T as ``decode_linear``, and ids[m] = argmax(logits[m]) (int64,
+    torch.argmax's tie and NaN conventions) -- the head and the greedy choice of a decode
+    step (mm_decode_head_argmax).  Returns the logits."""
+    dev = _lib.require_cuda(x, w, out, ids)
+    prm = _base(x, w, LIN_STORE)
+    if out is None:
+        out = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=dev)
+    if out.shape != (x.shape[0], w.shape[0]) or out.stride(1) != 1 or out.dtype != x.dtype:
+        raise ValueError("out must be (M, N) with x's dtype and unit inner stride")
+    if ids.shape != (x.shape[0],) or ids.dtype != torch.int64 or not ids.is_contiguous():
+        raise ValueError("ids must be a contiguous int64 (M,) tensor")
+    prm.y, prm.ldy = out.data_ptr(), out.stride(0)
+    lib = _lib.load()
+    ws = _workspace(dev, lib.mm_decode_head_argmax_workspace_size(prm.M, prm.N, prm.K))
+    if ws is not None:
+        prm.workspace, prm.workspace_bytes = ws.data_ptr(), ws.numel()
+    with _lib.on_device(dev):
+        st = lib.mm_decode_head_argmax(ctypes.byref(prm), ids.data_ptr(), _lib.stream_of(dev))
+    _lib.check(st, "mm_decode_head_argmax")
     return out
 
 

@@ -16,8 +16,9 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from mamba_metal_amd.mamba_block import NORM_PENDING, MambaBlock
-from mamba_metal_amd.linear import decode_linear, decode_linear_ok
+from mamba_metal_amd.linear import decode_head_argmax, decode_linear, decode_linear_ok
 from mamba_metal_amd.norm import add_rmsnorm
+from mamba_metal_amd.sample import argmax_rows
 
 
 @dataclass
@@ -131,6 +132,29 @@ class MambaModel(nn.Module):
             # (B, d_model) rows: decode-sized row blocks take the weight-streaming head
             return self._head(h[:, -1, :])[:, None, :], convs, ssms
         return self._head(h), convs, ssms
+
+    def step_greedy(self, input_ids: torch.Tensor, conv_states, ssm_states, ids_out: torch.Tensor):
+        """``step(input_ids, conv_states, ssm_states, inplace=True)`` followed by the greedy
+        choice ids_out = argmax(logits[:, 0, :]) (generate.py:91-93), the head and the argmax
+        in one call (mm_decode_head_argmax) where the decode GEMM takes the head.  The
+        states are updated in place; ids_out may be input_ids (the embedding reads it
+        first).  Returns the logits (B, 1, vocab)."""
+        it = iter(zip(conv_states, ssm_states))
+
+        def mix(m, h, resid, nrm, nxt):
+            cs, ss = next(it)
+            if h is NORM_PENDING:
+                return m.step_2d(resid, cs, ss, resid=resid, next_norm=nxt, x_norm=nrm,
+                                 defer_norm=True)
+            return m.step_2d(h, cs, ss, resid=resid, next_norm=nxt, defer_norm=True)
+
+        h = self._run(input_ids.reshape(-1), mix, defer_norm=True)
+        E = self.embeddings.weight
+        if h.dim() == 2 and decode_linear_ok(h, E):
+            return decode_head_argmax(h, E, ids_out)[:, None, :]
+        logits = self._head(h)
+        argmax_rows(logits if logits.stride(-1) == 1 else logits.contiguous(), out=ids_out)
+        return logits[:, None, :]
 
     def step(self, input_ids: torch.Tensor, conv_states, ssm_states, inplace: bool = False):
         """One new token per sequence (B, 1) -> (logits (B, 1, vocab), states).

@@ -48,7 +48,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_version_and_status_names(lib):
-    assert lib.mm_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.mm_abi_version() == _lib.ABI_VERSION == 5
     assert lib.mm_status_name(0) == b"MM_OK"
     assert lib.mm_status_name(-3) == b"MM_ERR_DSTATE"
     assert lib.mm_status_name(-99) == b"MM_ERR_UNKNOWN"
@@ -258,9 +258,9 @@ def test_decode_in_proj_xproj_validation(lib):
     assert call(xp_w=FAKE + 8) == _lib.ERR_LAYOUT
     assert call(n_conv=5100, ldc=5100) == _lib.ERR_LAYOUT    # x_proj's K must be a multiple of 64
     assert call(conv_out=FAKE + 8) == _lib.ERR_LAYOUT
-    # the fused path needs its partial planes (80 x 64 x 192 fp32 here)
+    # the fused path needs its partial planes (one 64 x 192 fp32 plane per 32 conv columns)
     need = lib.mm_decode_in_proj_xproj_workspace_size(64, 10240, 2560, 5120, 192)
-    assert need >= 80 * 64 * 192 * 4
+    assert need >= 160 * 64 * 192 * 4
     assert call() == _lib.ERR_WORKSPACE
     assert call(workspace=FAKE, workspace_bytes=need - 1) == _lib.ERR_WORKSPACE
     assert call(M=0) == _lib.OK
@@ -268,6 +268,35 @@ def test_decode_in_proj_xproj_validation(lib):
     assert lib.mm_decode_in_proj_xproj_workspace_size(2, 10240, 2560, 5120, 192) == \
         lib.mm_decode_linear_workspace_size(2, 192, 5120)
     assert lib.mm_decode_in_proj_xproj_workspace_size(0, 10240, 2560, 5120, 192) == 0
+
+
+def test_decode_head_argmax_validation(lib):
+    """mm_decode_head_argmax: the head params as for mm_decode_linear (plain store) plus the
+    int64 ids; the fused path keeps one (value, column) candidate per workgroup and row in
+    the workspace.  All checked before any launch."""
+    def call(ids=FAKE, **kw):
+        prm = _lib.LinearParams()
+        prm.x = prm.w_packed = prm.y = FAKE
+        prm.M, prm.N, prm.K = 64, 50280, 2560
+        prm.ldx, prm.ldy = 2560, 50280
+        prm.dtype, prm.epilogue = _lib.F16, 0
+        for k, v in kw.items():
+            setattr(prm, k, v)
+        return lib.mm_decode_head_argmax(ctypes.byref(prm), ids, None)
+    assert lib.mm_decode_head_argmax(None, FAKE, None) == _lib.ERR_NULL_POINTER
+    assert call(ids=None) == _lib.ERR_NULL_POINTER
+    assert call(ids=FAKE + 4) == _lib.ERR_LAYOUT
+    assert call(epilogue=1) == _lib.ERR_SHAPE
+    assert call(ldy=50000) == _lib.ERR_LAYOUT
+    assert call(M=65) == _lib.ERR_SHAPE
+    need = lib.mm_decode_head_argmax_workspace_size(64, 50280, 2560)
+    assert need == 197 * 64 * 8       # 197 workgroups of 8 x 32 columns
+    assert call() == _lib.ERR_WORKSPACE
+    assert call(workspace=FAKE, workspace_bytes=need - 1) == _lib.ERR_WORKSPACE
+    assert call(M=0) == _lib.OK
+    # narrow N (no shared-X head): mm_decode_linear's workspace, then mm_argmax_rows
+    assert lib.mm_decode_head_argmax_workspace_size(4, 3072, 768) == \
+        lib.mm_decode_linear_workspace_size(4, 3072, 768)
 
 
 def test_argmax_validation(lib):

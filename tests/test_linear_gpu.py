@@ -295,3 +295,46 @@ def test_decode_linear_small_m(dev, M, K, N, dtype):
     torch.cuda.synchronize()
     _check(y, _ref(x, w), dtype, f"gemv M={M} K={K} N={N}")
     assert torch.equal(y, decode_linear(x, w))      # deterministic
+
+
+# LM head + greedy argmax in one call (mm_decode_head_argmax): the logits equal
+# decode_linear's bit for bit and the ids equal argmax_rows on them.  Shapes: the 130M head
+# at batch 1 and 4 and the 2.8B head at batch 64 (shared-X kernel, candidates in its
+# epilogue), a narrow N (GEMV / linear_kernel, then mm_argmax_rows); planted ties (two
+# equal weight rows: the lower column wins) and a NaN column (it wins, the first of two).
+@pytest.mark.parametrize("M,K,N", [(1, 768, 50280), (4, 768, 50280), (64, 2560, 50280),
+                                   (8, 512, 3000)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_head_argmax(dev, M, K, N, dtype):
+    from mamba_metal_amd.linear import decode_head_argmax, decode_linear
+    from mamba_metal_amd.sample import argmax_rows
+
+    g = torch.Generator(device=dev).manual_seed(M + K + N)
+    x = torch.randn((M, K), generator=g, device=dev).to(dtype)
+    w = (torch.randn((N, K), generator=g, device=dev) * 0.05).to(dtype)
+    ids = torch.empty((M,), dtype=torch.int64, device=dev)
+    logits = decode_head_argmax(x, w, ids)
+    ref = decode_linear(x, w)
+    torch.cuda.synchronize()
+    assert torch.equal(logits, ref)
+    assert torch.equal(ids, argmax_rows(ref))
+    assert torch.equal(ids, ref.float().argmax(dim=1))
+    # ties: every row's winner duplicated at a lower and a higher column
+    top = ids.clone()
+    w2 = w.clone()
+    lo = int(top.min())
+    w2[max(lo - 7, 0)] = w2[lo]          # a lower column with the same weights as row lo
+    w2[N - 1] = w2[lo]
+    ids2 = torch.empty_like(ids)
+    lg2 = decode_head_argmax(x, w2, ids2)
+    torch.cuda.synchronize()
+    assert torch.equal(ids2, argmax_rows(lg2))
+    assert torch.equal(ids2, lg2.float().argmax(dim=1))
+    # NaN columns: the first one wins on every row
+    w3 = w.clone()
+    w3[N // 3, 0] = float("nan")
+    w3[N // 2, 0] = float("nan")
+    ids3 = torch.empty_like(ids)
+    decode_head_argmax(x, w3, ids3)
+    torch.cuda.synchronize()
+    assert torch.equal(ids3, torch.full_like(ids3, N // 3))
