@@ -619,15 +619,6 @@ __global__ __launch_bounds__(256) void xp_reduce_kernel(const LinParams p, int64
   }
 }
 
-// Shared-X kernel for wide N.  Workgroup = NW waves; wave w owns the 32 columns
-// n0 = (blockIdx.x * NW + w) * 32 and all of K.  Per 64-k chunk the waves load the
-// X chunk together (8 rows per load instruction, instruction q by wave q % NW), write
-// it to one of three LDS buffers and meet at a barrier; each wave then runs its 4 x MT
-// MFMAs from that buffer.  W and X loads run two chunks ahead of the MFMAs through a
-// three-slot register ring (named slots: an array indexed by slot would be moved to
-// scratch or LDS).  A buffer is rewritten three chunks after it was read, i.e. after
-// two more barriers, by which time every wave's reads of it have completed.  The
-// epilogue stores straight from the accumulators: lane l holds column n0 + l % 32.
 // a better than b for a greedy argmax: NaN first, then the larger value, then the lower
 // index (torch.argmax's conventions, as mm_argmax_rows).
 __device__ __forceinline__ bool arg_better(float av, int32_t ai, float bv, int32_t bi) {
@@ -683,6 +674,15 @@ __global__ __launch_bounds__(256) void head_argmax_kernel(const float* __restric
   }
 }
 
+// Shared-X kernel for wide N.  Workgroup = NW waves; wave w owns the 32 columns
+// n0 = (blockIdx.x * NW + w) * 32 and all of K.  Per 64-k chunk the waves load the
+// X chunk together (8 rows per load instruction, instruction q by wave q % NW), write
+// it to one of three LDS buffers and meet at a barrier; each wave then runs its 4 x MT
+// MFMAs from that buffer.  W and X loads run two chunks ahead of the MFMAs through a
+// three-slot register ring (named slots: an array indexed by slot would be moved to
+// scratch or LDS).  A buffer is rewritten three chunks after it was read, i.e. after
+// two more barriers, by which time every wave's reads of it have completed.  The
+// epilogue stores straight from the accumulators: lane l holds column n0 + l % 32.
 template <int XPW>
 struct ShareSlot {
   u32x4 w[kSteps];
