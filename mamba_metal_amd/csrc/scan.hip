@@ -8,8 +8,10 @@
 // Work decomposition
 //   * A workgroup owns a block of channels of one batch row.  dstate <= 16: 32 channels
 //     and 4 waves; lane l takes channel l % 32 and the two half-waves of wave g take
-//     state groups g and g + 4 of SPL = 2 states (8 groups cover 16 states).  dstate >
-//     16: 64 channels (one per lane) and 4 waves of SPL = 8 or 16 states.  Each lane
+//     state groups g and g + 4 of SPL = 2 states (8 groups cover 16 states); for some
+//     chain counts 48 channels and 6 waves, or 16 channels and 4 waves whose quarter-waves
+//     take one state each (see use_48, prefer_single_state).  dstate > 16: 64 channels
+//     (one per lane) and 4 waves of SPL = 8 or 16 states.  Each lane
 //     walks time SEQUENTIALLY with its SPL states in fp32 registers: the recurrence
 //     costs one exp2 and four VALU ops per (channel, state, step), with no parallel-scan
 //     overhead.
@@ -41,12 +43,14 @@ namespace mm {
 namespace scan {
 
 // Channels per workgroup: 64 (lane = channel) or, for the chained scan at dstate <= 16,
-// 32 (each half-wave takes the 32 channels with its own states).  kCpwMin sizes what
+// 32 (each half-wave takes the 32 channels with its own states), 48 (6 waves) or 16
+// (each quarter-wave takes the 16 channels with its own state).  kCpwMin sizes what
 // depends on the count of channel blocks (flags, tickets), kCpwMax what depends on the
 // padded channel count.
 constexpr int kCpwMax = 64;
-constexpr int kCpwMin = 32;
-// dstate <= 16: 8 state groups of 2 states (dstate <= 8: of 1 state).
+constexpr int kCpwMin = 16;
+// dstate <= 16: 8 state groups of 2 states (dstate <= 8: of 1 state); the 16-channel
+// block runs 16 groups of 1 state (see prefer_single_state).
 constexpr int kGroups16 = 8;
 constexpr int kSpl16 = 2;
 
@@ -152,6 +156,31 @@ inline void pick_shape(int64_t dstate, int* groups, int* spl) {
   }
 }
 
+// Between one and two 32-channel chains per CU half the CUs would run two chains, which
+// then set the critical path.  48-channel blocks of 6 waves make it one chain per CU where
+// that many fit; their carries fit the workspace's 64-channel layout when dim rounds up
+// no further for 48 than for 64.
+inline bool use_48(int64_t batch, int64_t dim, int64_t cus) {
+  return batch * ceil_div(dim, 32) > cus && batch * ceil_div(dim, 48) <= cus &&
+         round_up(dim, 48) <= round_up(dim, 64);
+}
+
+// Time-contiguous dstate 9..16 scans with 2-3 chains per CU in 16-channel blocks that
+// neither the 48-channel blocks nor the split scan take run 16-channel blocks with one
+// state per lane: three resident workgroups of 4 waves per CU then hold three chains per
+// CU (3 waves per SIMD), where 32-channel blocks leave half the CUs two chains.  Measured
+// against the 32-channel blocks (fp16, L=8192): B=1 D=8704 0.565 -> 0.500 ms, B=2 D=5120
+// 0.59 -> 0.545, B=3 D=4096 0.588 -> 0.557.  It loses where the recurrence is VALU-bound
+// or the 48-channel blocks apply, its single state per lane giving the scheduler half the
+// independent work: B=4 D=5120 L=32768 2.79 -> 3.18 ms, B=64 D=5120 L=512 0.69 -> 0.84,
+// B=8 D=1536 L=8192 0.64 (48-channel) -> 0.68.  A lane's update costs the same five VALU
+// instructions; per (channel, step) the epilogue sums 16 partial y's instead of 8.
+inline bool prefer_single_state(int64_t batch, int64_t dim, int64_t seqlen, int64_t cus) {
+  const int64_t ncb16 = batch * ceil_div(dim, 16);
+  return ncb16 > 2 * cus && ncb16 <= 3 * cus && !use_48(batch, dim, cus) &&
+         !split_capable(batch * ceil_div(dim, 64), kGroups16, seqlen);
+}
+
 // ---------------------------------------------------------------------------
 // B/C pack: bc[((b*G + g)*Lp + t)*2*SPL + k]       = ln2 * B[b, g*SPL + k, t]
 //           bc[((b*G + g)*Lp + t)*2*SPL + SPL + k] = C[b, g*SPL + k, t]
@@ -237,9 +266,10 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
   using T = typename Ty<DT>::T;
   // CPW channels per workgroup and GS = 64 G / CPW state groups.  CPW = 64: lane l takes
   // channel l, wave g state group g.  CPW = 32: the two half-waves take the same
-  // channels and different states (state groups g and g + G).  CPW = 48 (6 waves):
+  // channels and different states (state groups g and g + G); CPW = 16 likewise with
+  // four quarter-waves (state groups g, g + G, g + 2G, g + 3G).  CPW = 48 (6 waves):
   // thread t takes channel t % 48 and state group t / 48.
-  static_assert(CPW == 64 || CPW == 48 || CPW == 32, "channel block");
+  static_assert(CPW == 64 || CPW == 48 || CPW == 32 || CPW == 16, "channel block");
   constexpr int NT = 64 * G;
   static_assert(NT % CPW == 0, "whole state groups per workgroup");
   constexpr int GS = NT / CPW;
@@ -277,8 +307,8 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
                                    : t * CPW + c;
   };
   // B/C of the tile, one row of kT steps x (SPL B, SPL C) per state group.  A 32-channel
-  // block's half-waves read two groups G rows apart in one instruction: the 4-float pad
-  // puts those rows on different banks.
+  // block's half-waves read two groups G rows apart in one instruction (a 16-channel
+  // block's quarter-waves four): the 4-float pad puts those rows on different banks.
   constexpr int BCR = kT * 2 * SPL + 4;
   __shared__ __attribute__((aligned(16))) float s_bc[GS][BCR];
   __shared__ int s_ticket;
@@ -823,13 +853,9 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
     // 768 vs 1.46-1.47 at 512), with fewer the chains' segment order is the critical path
     // and spare workgroups take the next segments early (B=8 D=1536 L=8192: 0.605 ms at
     // 768, 0.627 at 512).
-    // Between one and two 32-channel chains per CU (B=8 D=1536: 384 chains on 256 CUs)
-    // half the CUs would run two chains, which then set the critical path; 48-channel
-    // blocks of 6 waves make it one chain per CU where that many fit (256 there).  The
-    // carries of 48-channel blocks fit the workspace's 64-channel layout when dim rounds
-    // up no further for 48 than for 64.
-    const int64_t ncb48 = a->batch * ceil_div(a->dim, 48);
-    if (p.ncb > cus && ncb48 <= cus && round_up(a->dim, 48) <= round_up(a->dim, 64)) {
+    // 48-channel blocks (see use_48), e.g. B=8 D=1536: 384 32-channel chains, 256
+    // 48-channel ones on 256 CUs
+    if (use_48(a->batch, a->dim, cus)) {
       auto k48 = scan_kernel<DT, LAYOUT, SPL, 6, VEC, kChained, 48>;
       static DeviceCache c48_cache;
       const int64_t r48 = cus * resident_per_cu(c48_cache, k48, 64 * 6);
@@ -839,6 +865,13 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
     }
     if (p.ncb >= 2 * cus && p.ncb < 4 * cus && r32 > 2 * cus) r32 = 2 * cus;
     launch_chained<DT, LAYOUT, SPL, GS / 2, VEC, 32>(p, a, s, w, r32);
+  } else if constexpr (GS == 16) {
+    // 16-channel blocks of 4 waves, one state per lane (see prefer_single_state)
+    auto k16 = scan_kernel<DT, LAYOUT, SPL, 4, VEC, kChained, 16>;
+    static DeviceCache c16_cache;
+    const int64_t r16 = cus * resident_per_cu(c16_cache, k16, 256);
+    set_blocks(p, a->batch, 16);
+    launch_chained<DT, LAYOUT, SPL, 4, VEC, 16>(p, a, s, w, r16);
   } else {
     auto kern = scan_kernel<DT, LAYOUT, SPL, GS, VEC, kChained, 64>;
     static DeviceCache per_cu_cache;
@@ -858,7 +891,7 @@ void launch(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& w)
 // for (ws_layout sizes the B/C pack and the carries by groups * spl): every shape
 // pick_shape can return has its own case, and anything else is an error.
 inline bool shape_known(int groups, int spl) {
-  return (groups == 8 && (spl == 1 || spl == 2)) ||
+  return (groups == 8 && (spl == 1 || spl == 2)) || (groups == 16 && spl == 1) ||
          (groups == 4 && (spl == 2 || spl == 4 || spl == 8 || spl == 16));
 }
 
@@ -867,6 +900,7 @@ void launch_shape(Params p, const mm_scan_params* a, hipStream_t s, const WsLayo
                   int spl) {
   if (groups == 8 && spl == 1) launch<DT, LAYOUT, 1, 8>(p, a, s, w);
   else if (groups == 8 && spl == 2) launch<DT, LAYOUT, 2, 8>(p, a, s, w);
+  else if (groups == 16 && spl == 1) launch<DT, LAYOUT, 1, 16>(p, a, s, w);
   else if (groups == 4 && spl == 2) launch<DT, LAYOUT, 2, 4>(p, a, s, w);
   else if (groups == 4 && spl == 4) launch<DT, LAYOUT, 4, 4>(p, a, s, w);
   else if (groups == 4 && spl == 8) launch<DT, LAYOUT, 8, 4>(p, a, s, w);
@@ -897,6 +931,7 @@ void launch_pack(const mm_scan_params* a, int64_t Lp, int groups, int spl, const
                      a->C_stride[1], a->C_stride[2])
   if (groups == 8 && spl == 1) MM_PACK(1, 8);
   else if (groups == 8 && spl == 2) MM_PACK(2, 8);
+  else if (groups == 16 && spl == 1) MM_PACK(1, 16);
   else if (groups == 4 && spl == 2) MM_PACK(2, 4);
   else if (groups == 4 && spl == 4) MM_PACK(4, 4);
   else if (groups == 4 && spl == 8) MM_PACK(8, 4);
@@ -968,9 +1003,15 @@ int fwd(const mm_scan_params* a, void* stream, bool chained_min_ok) {
   pick_shape(a->dstate, &groups, &spl);
   if (!shape_known(groups, spl))
     return fail(MM_ERR_DSTATE, "no scan instantiation for %d groups x %d states", groups, spl);
-  const int ept = kT / groups;  // elements per thread per tile, either channel block
   int layout = kTimeContig, vec_ok = 0;
-  choose_layout(a, ept, &layout, &vec_ok);
+  // elements per thread per tile: kT / groups for every channel block
+  choose_layout(a, kT / groups, &layout, &vec_ok);
+  if (groups == kGroups16 && spl == kSpl16 && layout == kTimeContig &&
+      prefer_single_state(a->batch, a->dim, a->seqlen, num_cus())) {
+    groups = 16;  // the same B/C and carry bytes as 8 x 2
+    spl = 1;
+    choose_layout(a, kT / groups, &layout, &vec_ok);
+  }
   const WsLayout w = ws_layout(a->batch, a->dim, groups, spl, std::max<int64_t>(a->seqlen, 1));
   const size_t need = chained_min_ok ? w.sum : w.total;
   if (a->workspace == nullptr || a->workspace_bytes < need)

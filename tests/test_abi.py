@@ -109,11 +109,11 @@ def test_scan_validation_errors(lib, over, status):
 
 
 def test_workspace_size(lib):
-    # control block (256 B) + one flag per 32-channel block + carried state (per
-    # 64-channel block) + packed fp32 B/C (16 states -> 8 groups x 2 per lane, padded to
-    # 32-step tiles)
+    # control block (256 B) + one flag per 16-channel block (the smallest channel block)
+    # + carried state (per 64-channel block) + packed fp32 B/C (16 states -> 8 groups x 2
+    # per lane, padded to 32-step tiles)
     ncb = 4 * 5120 // 64
-    flags_end = 256 + 4 * (4 * 5120 // 32)
+    flags_end = 256 + 4 * (4 * 5120 // 16)
     carry = -(-flags_end // 256) * 256
     bc = -(-(carry + 4 * ncb * 16 * 64) // 256) * 256
     assert lib.mm_selective_scan_workspace_size(4, 5120, 16, 32768) == bc + 4 * 4 * 16 * 32768 * 2
@@ -127,14 +127,14 @@ def test_workspace_size(lib):
     # fp32 per block
     small = 20992  # ctl/flags 512 + carry 4096 + B/C 16384 (one 128-step padded row)
     assert lib.mm_selective_scan_workspace_size(1, 64, 16, 100) == small + 4 * 256 * (16 * 64 + 64)
-    # 128 blocks: 32 segments each (ctl + 256 flags 1280 B, carry 524288, B/C 2097152)
+    # 128 blocks: 32 segments each (ctl + 512 flags 2304 B, carry 524288, B/C 2097152)
     assert lib.mm_selective_scan_workspace_size(128, 64, 16, 100) == \
-        1280 + 524288 + 2097152 + 4 * 128 * 32 * (16 * 64 + 64)
+        2304 + 524288 + 2097152 + 4 * 128 * 32 * (16 * 64 + 64)
     # 129..256 blocks: summaries only for sequences of >= 512 tiles (16384 steps):
     # 2 x 5120 = 160 blocks, 4096 // 160 = 25 segments each
     def base(batch, dim, L):
         up = lambda v, a: -(-v // a) * a
-        carry = up(256 + 4 * batch * (-(-dim // 32)), 256)
+        carry = up(256 + 4 * batch * (-(-dim // 16)), 256)
         bc = up(carry + 4 * batch * (-(-dim // 64)) * 16 * 64, 256)
         return up(bc + 4 * batch * 8 * up(L, 128) * 4, 256)
     assert lib.mm_selective_scan_workspace_size(2, 5120, 16, 16384) == \

@@ -6,7 +6,7 @@ Cases restate the reference's own scan checks, now with assertions:
   18-prefill/verify_state_out (final state)
 plus edge shapes, strided layouts, dtypes, determinism and the BASELINE
 configs (config 0 against the committed golden fixture; configs 2 and 4 at full
-size with one channel of every 32-channel block against the oracle -- channels are
+size with one channel of every 16-channel block against the oracle -- channels are
 independent, so any subset must match the oracle run on that subset alone).
 
 Tolerances (from the task's parity bar): fp32 rtol 1e-5 (atol 1e-5 for |y| ~ 0);
@@ -206,6 +206,33 @@ def test_48_channel_blocks(oracle_lib, dev, layout):
           layout=layout)
 
 
+def _single_state_dim(cus, batch):
+    """A ragged dim (16 k - 8) whose time-contiguous scan runs the 16-channel blocks of one
+    state per lane on a part with `cus` CUs: 2 cus < batch * k <= 3 cus 16-channel chains,
+    more than `cus` 48-channel ones (so not the 48-channel blocks) and more than 128
+    64-channel ones (no split scan at short lengths)."""
+    for k in range(2 * cus // batch + 1, 3 * cus // batch + 1):
+        dim = 16 * k - 8
+        if batch * -(-dim // 48) > cus and batch * -(-dim // 64) > 128:
+            return dim
+    pytest.skip(f"no ragged 16-channel-block shape at batch {batch} on {cus} CUs")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("seqlen", [300, 301])
+def test_16_channel_blocks_ragged(oracle_lib, dev, dtype, seqlen):
+    """16-channel blocks (one state per lane) with a partial last block (dim = 16 k - 8,
+    4088 at batch 3 on 256 CUs) and a sequence ending inside a tile; an odd length takes the
+    element-wise (non-vector) loads.  dstate 16 and 12 (padded states)."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    dim = _single_state_dim(cus, 3)
+    for n, seed in ((16, 16), (12, 12)):
+        inp = fp16_inputs(3, dim, n, seqlen, seed=seed) if dtype != torch.float32 else \
+            features_inputs(3, dim, n, seqlen, seed=seed)
+        check(oracle_lib, dev, inp, f"16-channel blocks N={n} L={seqlen} {dtype}", dtype=dtype,
+              softplus=True)
+
+
 def test_channel_contiguous_views_keep_their_layout(oracle_lib, dev):
     """Transposed (batch, seqlen, dim) views in: y comes back in the same layout (so the
     kernel's channel-contiguous path runs end to end) with the oracle's values."""
@@ -288,10 +315,10 @@ def test_config0_against_golden(dev):
 
 
 def _blockwise_parity(oracle_lib, dev, batch, dim, seqlen, seed, dtype=torch.float16):
-    """Full-size fp16 (or bf16) scan on the GPU; the fp64 oracle on one channel of EVERY 32-channel
+    """Full-size fp16 (or bf16) scan on the GPU; the fp64 oracle on one channel of EVERY 16-channel
     block (a random lane per block, plus the first and last channel): the kernel's
-    chains are blocks of 64 or 32 channels, each with its own segment hand-offs, so every
-    chain's hand-offs are checked.  Channels are independent, so a subset must match the
+    chains are blocks of 64, 48, 32 or 16 channels, each with its own segment hand-offs, so
+    every chain's hand-offs are checked.  Channels are independent, so a subset must match the
     oracle run on that subset."""
     from mamba_metal_amd import selective_scan
     from mamba_metal_amd.selective_scan import reset_scan_status, scan_status
@@ -312,10 +339,10 @@ def _blockwise_parity(oracle_lib, dev, batch, dim, seqlen, seed, dtype=torch.flo
     assert scan_status(dev) == 0    # every segment hand-off completed
     assert torch.isfinite(y).all()
     rng = np.random.default_rng(seed)
-    nblk = -(-dim // 32)
+    nblk = -(-dim // 16)
     checked = 0
     for b in range(batch):
-        chans = np.minimum(np.arange(nblk) * 32 + rng.integers(0, 32, nblk), dim - 1)
+        chans = np.minimum(np.arange(nblk) * 16 + rng.integers(0, 16, nblk), dim - 1)
         chans = np.unique(np.concatenate([chans, [0, dim - 1]]))
         idx = torch.as_tensor(chans, device=dev)
         pick = lambda t: t[b:b + 1].index_select(1, idx).float().cpu().numpy()
@@ -398,13 +425,13 @@ def test_split_lone_chain_many_segments(oracle_lib, dev):
 
 def test_split_few_chains_full_length(oracle_lib, dev):
     """B=1, D=5120, L=32768 fp16 (80 64-channel blocks: the split path with up to 51
-    segments per chain), one channel of every 32-channel block against the oracle."""
+    segments per chain), one channel of every 16-channel block against the oracle."""
     _blockwise_parity(oracle_lib, dev, 1, 5120, 32768, seed=5)
 
 
 def test_split_long_sequence_160_blocks(oracle_lib, dev):
     """B=2, D=5120, L=32768 fp16: 160 64-channel blocks take the split path only because
-    the sequence is long (25 segment summaries per block), one channel of every 32-channel
+    the sequence is long (25 segment summaries per block), one channel of every 16-channel
     block against the oracle."""
     _blockwise_parity(oracle_lib, dev, 2, 5120, 32768, seed=6)
 
@@ -419,9 +446,15 @@ def test_grid_regime_boundaries(oracle_lib, dev, dim, seqlen):
 
 
 def test_bf16_large_every_block(oracle_lib, dev):
-    """bf16 inputs and output at B=2 D=5120 L=8192 (320 32-channel chains, the two
-    workgroups per CU grid): one channel of every block against the oracle."""
+    """bf16 inputs and output at B=2 D=5120 L=8192 (640 16-channel chains of one state per
+    lane on 256 CUs): one channel of every block against the oracle."""
     _blockwise_parity(oracle_lib, dev, 2, 5120, 8192, seed=7, dtype=torch.bfloat16)
+
+
+def test_16_channel_blocks_full_length_every_block(oracle_lib, dev):
+    """B=1 D=8704 L=8192 fp16 (544 16-channel chains of one state per lane on 256 CUs, four
+    segment hand-offs each): one channel of every block against the oracle."""
+    _blockwise_parity(oracle_lib, dev, 1, 8704, 8192, seed=17)
 
 
 def test_config2_full_size_every_block(oracle_lib, dev):
