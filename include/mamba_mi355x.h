@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 5
+#define MM_ABI_VERSION 6
 /* Largest d_state accepted: mamba_metal/selective_scan.py:9 (MAX_DSTATE = 64). */
 #define MM_MAX_DSTATE 64
 
@@ -338,6 +338,16 @@ int mm_decode_in_proj_xproj(const mm_linear_params* params, const void* xp_w_pac
  * params->workspace must hold mm_decode_head_argmax_workspace_size bytes. */
 size_t mm_decode_head_argmax_workspace_size(int64_t M, int64_t N, int64_t K);
 int mm_decode_head_argmax(const mm_linear_params* params, int64_t* ids, void* stream);
+
+/* mm_decode_head_argmax, then the next step's embedding lookup -- replaces generate.py's
+ * feeding of the chosen ids back through the embedding (mamba_model.py:75,
+ * self.embedding(input_ids)): rows[m, k] = table[ids[m], k] for k < params->K.  table is
+ * the (N, K) embedding matrix the head is tied to, row-major with row stride ld_table;
+ * rows has row stride ld_rows; both 2-byte elements, strides multiples of 8 (>= K),
+ * 16-byte aligned, rows not overlapping x or y.  On the fused head path the copy runs
+ * in the kernel that picks the ids. */
+int mm_decode_head_argmax_embed(const mm_linear_params* params, int64_t* ids, const void* table,
+                                int64_t ld_table, void* rows, int64_t ld_rows, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Prefill projection GEMM for short K -- replaces the dt projection of the parallel

@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library; see module d
 
 LIB_NAME = "libmamba_mi355x.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 5
+ABI_VERSION = 6
 MAX_DSTATE = 64
 
 # mm_dtype
@@ -104,6 +104,8 @@ _SIGNATURES = {
     "mm_decode_linear": ([ctypes.POINTER(LinearParams), _vp], ctypes.c_int),
     "mm_decode_head_argmax_workspace_size": ([_i64, _i64, _i64], _sz),
     "mm_decode_head_argmax": ([ctypes.POINTER(LinearParams), _vp, _vp], ctypes.c_int),
+    "mm_decode_head_argmax_embed": ([ctypes.POINTER(LinearParams), _vp, _vp, _i64, _vp, _i64, _vp],
+                                    ctypes.c_int),
     "mm_decode_in_proj_xproj_workspace_size": ([_i64] * 5, _sz),
     "mm_decode_in_proj_xproj": ([ctypes.POINTER(LinearParams), _vp, _i64, _vp, _i64, _vp],
                                 ctypes.c_int),

@@ -628,14 +628,34 @@ __device__ __forceinline__ bool arg_better(float av, int32_t ai, float bv, int32
   return ai < bi;
 }
 
+// mm_decode_head_argmax_embed: rows[m, :len] = table[ids[m], :len] (2-byte elements,
+// len, both row strides multiple of 8 and 16-byte aligned rows: 8-element copies).
+struct EmbedArgs {
+  const u32x4* table;
+  int64_t ld_table;
+  u32x4* rows;
+  int64_t ld_rows;
+  int64_t len;
+};
+
+// The embedding row of id into row r, copied by the workgroup's 256 threads.
+__device__ __forceinline__ void copy_embed_row(const EmbedArgs& e, int64_t r, int64_t id, int tid) {
+  const u32x4* const src = e.table + id * (e.ld_table / 8);
+  u32x4* const dst = e.rows + r * (e.ld_rows / 8);
+  for (int64_t c = tid; c < e.len / 8; c += 256) dst[c] = src[c];
+}
+
 // Second pass of mm_decode_head_argmax: one workgroup per row picks among the nwg
-// workgroup candidates (in that order, so ties keep the lowest column).
+// workgroup candidates (in that order, so ties keep the lowest column); with an
+// embedding table (e.table) it then writes the chosen id's embedding row.
 __global__ __launch_bounds__(256) void head_argmax_kernel(const float* __restrict__ cand_v,
                                                           const int32_t* __restrict__ cand_i,
                                                           int64_t nwg, int64_t M,
-                                                          int64_t* __restrict__ ids) {
+                                                          int64_t* __restrict__ ids,
+                                                          const EmbedArgs e) {
   __shared__ float s_v[4];
   __shared__ int32_t s_i[4];
+  __shared__ int32_t s_id;
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x;
   float bv = -__builtin_inff();
@@ -671,7 +691,19 @@ __global__ __launch_bounds__(256) void head_argmax_kernel(const float* __restric
         bi = s_i[w];
       }
     ids[r] = bi;
+    s_id = bi;
   }
+  if (e.table != nullptr) {
+    __syncthreads();
+    copy_embed_row(e, r, s_id, tid);
+  }
+}
+
+// mm_decode_head_argmax_embed after a separate argmax (heads the fused path does not
+// take): one workgroup per row copies the embedding row of ids[row].
+__global__ __launch_bounds__(256) void embed_rows_kernel(const int64_t* __restrict__ ids,
+                                                         const EmbedArgs e) {
+  copy_embed_row(e, blockIdx.x, ids[blockIdx.x], threadIdx.x);
 }
 
 // Shared-X kernel for wide N.  Workgroup = NW waves; wave w owns the 32 columns
@@ -1540,7 +1572,7 @@ inline size_t head_cand_bytes(int64_t M, int64_t N, int64_t K) {
 }
 
 static int decode_linear_core(const mm_linear_params* prm, void* stream, const XpArgs* xp,
-                              int64_t* argmax_ids = nullptr) {
+                              int64_t* argmax_ids = nullptr, const EmbedArgs* embed = nullptr) {
   if (!prm) return fail(MM_ERR_NULL_POINTER, "params is NULL");
   const mm_linear_params& q = *prm;
   if (!q.x || !q.w_packed) return fail(MM_ERR_NULL_POINTER, "x and w_packed are required");
@@ -1644,8 +1676,10 @@ static int decode_linear_core(const mm_linear_params* prm, void* stream, const X
   if (fuse_argmax) {
     if (q.dtype == MM_F16) launch_share<MM_F16>(p, kStoreArgmax, pl, grid, s);
     else launch_share<MM_BF16>(p, kStoreArgmax, pl, grid, s);
+    const EmbedArgs none{nullptr, 0, nullptr, 0, 0};
     hipLaunchKernelGGL(head_argmax_kernel, dim3(static_cast<unsigned>(q.M)), dim3(256), 0, s,
-                       p.cand_v, p.cand_i, static_cast<int64_t>(grid.x), q.M, argmax_ids);
+                       p.cand_v, p.cand_i, static_cast<int64_t>(grid.x), q.M, argmax_ids,
+                       embed ? *embed : none);
     return check_launch("decode_head_argmax");
   }
   if (use_gemv(q.M, q.N)) {
@@ -1695,10 +1729,14 @@ size_t mm_decode_head_argmax_workspace_size(int64_t M, int64_t N, int64_t K) {
   return head_fusable(M, N, K) ? std::max(lin, head_cand_bytes(M, N, K)) : lin;
 }
 
-int mm_decode_head_argmax(const mm_linear_params* prm, int64_t* ids, void* stream) {
-  using namespace mm;
-  using namespace mm::gemm;
-  clear_error();
+}  // extern "C"
+
+namespace mm {
+namespace gemm {
+
+// mm_decode_head_argmax[_embed] (embed may be NULL).
+static int head_argmax(const mm_linear_params* prm, int64_t* ids, const EmbedArgs* embed,
+                       void* stream) {
   if (!prm) return fail(MM_ERR_NULL_POINTER, "params is NULL");
   if (!ids) return fail(MM_ERR_NULL_POINTER, "ids is required");
   if (prm->epilogue != MM_LIN_STORE) return fail(MM_ERR_SHAPE, "the head takes the MM_LIN_STORE epilogue");
@@ -1706,10 +1744,40 @@ int mm_decode_head_argmax(const mm_linear_params* prm, int64_t* ids, void* strea
   if (prm->ldy < prm->N) return fail(MM_ERR_LAYOUT, "ldy < N");
   if (!aligned(ids, 8)) return fail(MM_ERR_LAYOUT, "ids must be 8-byte aligned");
   if (!prm->x_norm_w && head_fusable(prm->M, prm->N, prm->K))
-    return decode_linear_core(prm, stream, nullptr, ids);
-  const int st = decode_linear_core(prm, stream, nullptr);
+    return decode_linear_core(prm, stream, nullptr, ids, embed);
+  int st = decode_linear_core(prm, stream, nullptr);
   if (st != MM_OK || prm->M == 0 || prm->N == 0) return st;
-  return mm_argmax_rows(prm->y, prm->M, prm->N, prm->ldy, prm->dtype, ids, stream);
+  st = mm_argmax_rows(prm->y, prm->M, prm->N, prm->ldy, prm->dtype, ids, stream);
+  if (st != MM_OK || embed == nullptr) return st;
+  hipLaunchKernelGGL(embed_rows_kernel, dim3(static_cast<unsigned>(prm->M)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), ids, *embed);
+  return check_launch("decode_head_argmax_embed");
+}
+
+}  // namespace gemm
+}  // namespace mm
+
+extern "C" {
+
+int mm_decode_head_argmax(const mm_linear_params* prm, int64_t* ids, void* stream) {
+  mm::clear_error();
+  return mm::gemm::head_argmax(prm, ids, nullptr, stream);
+}
+
+int mm_decode_head_argmax_embed(const mm_linear_params* prm, int64_t* ids, const void* table,
+                                int64_t ld_table, void* rows, int64_t ld_rows, void* stream) {
+  using namespace mm;
+  using namespace mm::gemm;
+  clear_error();
+  if (!prm) return fail(MM_ERR_NULL_POINTER, "params is NULL");
+  if (!table || !rows) return fail(MM_ERR_NULL_POINTER, "table and rows are required");
+  if (ld_table < prm->K || ld_rows < prm->K || ld_table % 8 != 0 || ld_rows % 8 != 0 ||
+      prm->K % 8 != 0 || !aligned(table, 16) || !aligned(rows, 16))
+    return fail(MM_ERR_LAYOUT, "table and rows: row strides >= K (=%lld), multiples of 8, "
+                "16-byte aligned", (long long)prm->K);
+  const EmbedArgs e{static_cast<const u32x4*>(table), ld_table, static_cast<u32x4*>(rows),
+                    ld_rows, prm->K};
+  return head_argmax(prm, ids, &e, stream);
 }
 
 size_t mm_decode_in_proj_xproj_workspace_size(int64_t M, int64_t N, int64_t K, int64_t n_conv,

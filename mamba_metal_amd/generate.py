@@ -167,7 +167,9 @@ class GraphDecoder:
     steps, ``step()`` hands their ids out one per call (the same ids, in the same order,
     as K = 1), and the resident state runs up to K - 1 steps ahead of the ids returned.
     The K steps pass their ids through a ring of K rows: step j reads row j - 1 (mod K)
-    and its argmax writes row j.
+    and its argmax writes row j.  The embedding row of the next step's ids is written by
+    the same kernel that picks them (``step_greedy(hidden=...)``), so no step runs an
+    embedding lookup of its own.
     """
 
     def __init__(self, model, batch_size: int, use_graph: bool = True, steps_per_graph: int = 1):
@@ -178,6 +180,7 @@ class GraphDecoder:
         self.graph = None
         self.ids = None
         self.ring = None     # (K, B) ids of one replay (K > 1)
+        self.hid = None      # (B, d_model) embedding rows of the next step's input ids
         self.pending = 0     # ids of the last replay not yet handed out
         self.convs = None
         self.ssms = None
@@ -187,7 +190,7 @@ class GraphDecoder:
         """One decode step on input ids ``src``; its greedy ids go to ``dst`` (which may be
         ``src``: the embedding reads it before the argmax writes).  The head and the
         argmax run as one call (``MambaModel.step_greedy``)."""
-        self.model.step_greedy(src.view(-1, 1), self.convs, self.ssms, dst)
+        self.model.step_greedy(src.view(-1, 1), self.convs, self.ssms, dst, hidden=self.hid)
         return dst
 
     def _eager_step(self):
@@ -224,6 +227,11 @@ class GraphDecoder:
         if self.ring is not None:
             self.ring[self.k - 1].copy_(first)  # the next replay's first input
             self.pending = 0
+        rows = self.model.embeddings(first)
+        if self.hid is None:
+            self.hid = rows
+        else:
+            self.hid.copy_(rows)
         if self.use_graph and self.graph is None:
             self._capture()
         return first
@@ -231,7 +239,8 @@ class GraphDecoder:
     def _capture(self):
         # Warm up on a side stream (lazy library init, hipBLASLt heuristics), then
         # restore the state the warm-up step advanced.
-        bufs = self.convs + self.ssms + [self.ids] + ([self.ring] if self.ring is not None else [])
+        bufs = self.convs + self.ssms + [self.ids, self.hid] + \
+            ([self.ring] if self.ring is not None else [])
         saved = [t.clone() for t in bufs]
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())

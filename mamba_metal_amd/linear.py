@@ -164,11 +164,13 @@ def decode_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = N
 
 
 def decode_head_argmax(x: torch.Tensor, w: torch.Tensor, ids: torch.Tensor,
-                       out: torch.Tensor | None = None):
+                       out: torch.Tensor | None = None, embed_out: torch.Tensor | None = None):
     """logits (M, N) = x @ w.T as ``decode_linear``, and ids[m] = argmax(logits[m]) (int64,
     torch.argmax's tie and NaN conventions) -- the head and the greedy choice of a decode
-    step (mm_decode_head_argmax).  Returns the logits."""
-    dev = _lib.require_cuda(x, w, out, ids)
+    step (mm_decode_head_argmax).  With ``embed_out`` (M, K) the tied embedding rows of
+    the chosen ids are written there too, embed_out[m] = w[ids[m]] -- the next step's
+    input (mm_decode_head_argmax_embed).  Returns the logits."""
+    dev = _lib.require_cuda(x, w, out, ids, embed_out)
     prm = _base(x, w, LIN_STORE)
     if out is None:
         out = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=dev)
@@ -181,6 +183,15 @@ def decode_head_argmax(x: torch.Tensor, w: torch.Tensor, ids: torch.Tensor,
     ws = _workspace(dev, lib.mm_decode_head_argmax_workspace_size(prm.M, prm.N, prm.K))
     if ws is not None:
         prm.workspace, prm.workspace_bytes = ws.data_ptr(), ws.numel()
+    if embed_out is not None:
+        if embed_out.shape != x.shape or embed_out.dtype != w.dtype or not _rows_ok(embed_out):
+            raise ValueError("embed_out must be (M, K) in w's dtype with 16-byte aligned rows")
+        with _lib.on_device(dev):
+            st = lib.mm_decode_head_argmax_embed(ctypes.byref(prm), ids.data_ptr(), w.data_ptr(),
+                                                 w.stride(0), embed_out.data_ptr(),
+                                                 embed_out.stride(0), _lib.stream_of(dev))
+        _lib.check(st, "mm_decode_head_argmax_embed")
+        return out
     with _lib.on_device(dev):
         st = lib.mm_decode_head_argmax(ctypes.byref(prm), ids.data_ptr(), _lib.stream_of(dev))
     _lib.check(st, "mm_decode_head_argmax")

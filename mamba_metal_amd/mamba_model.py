@@ -80,7 +80,7 @@ class MambaModel(nn.Module):
             return decode_linear(h, E)
         return F.linear(h, E)
 
-    def _run(self, input_ids, mix, defer_norm: bool = False):
+    def _run(self, input_ids, mix, defer_norm: bool = False, resid=None):
         """Layer chain with the residual add fused into the next layer's RMSNorm:
         resid += y_prev; h = RMSNorm(resid) (one kernel per layer boundary).
         ``mix(mixer, h, resid, norm, next_norm)`` returns either ``(y, None)`` -- the
@@ -88,8 +88,11 @@ class MambaModel(nn.Module):
         output into ``resid`` and applied ``next_norm`` itself.  With ``defer_norm`` the
         first norm is not applied here (h = NORM_PENDING: the mixer applies ``norm`` to
         ``resid`` itself, in its first projection), and a mixer may return
-        ``(None, NORM_PENDING)`` to leave ``next_norm`` to the next one."""
-        resid = self.embeddings(input_ids)
+        ``(None, NORM_PENDING)`` to leave ``next_norm`` to the next one.  ``resid``, when
+        given, already holds the embedding rows of input_ids and becomes the residual
+        stream (updated in place)."""
+        if resid is None:
+            resid = self.embeddings(input_ids)
         norms = [layer.norm for layer in self.layers] + [self.norm_f]
         h = NORM_PENDING if defer_norm else add_rmsnorm(resid, None, norms[0].weight,
                                                         norms[0].eps)
@@ -133,12 +136,17 @@ class MambaModel(nn.Module):
             return self._head(h[:, -1, :])[:, None, :], convs, ssms
         return self._head(h), convs, ssms
 
-    def step_greedy(self, input_ids: torch.Tensor, conv_states, ssm_states, ids_out: torch.Tensor):
+    def step_greedy(self, input_ids: torch.Tensor, conv_states, ssm_states, ids_out: torch.Tensor,
+                    hidden: torch.Tensor | None = None):
         """``step(input_ids, conv_states, ssm_states, inplace=True)`` followed by the greedy
         choice ids_out = argmax(logits[:, 0, :]) (generate.py:91-93), the head and the argmax
         in one call (mm_decode_head_argmax) where the decode GEMM takes the head.  The
         states are updated in place; ids_out may be input_ids (the embedding reads it
-        first).  Returns the logits (B, 1, vocab)."""
+        first).  ``hidden`` (B, d_model), when given, holds the embedding rows of input_ids
+        on entry (the step uses it as its residual stream instead of looking them up) and
+        the embedding rows of ids_out on return, written by the argmax's kernel
+        (mm_decode_head_argmax_embed): consecutive steps then run no embedding lookup.
+        Returns the logits (B, 1, vocab)."""
         it = iter(zip(conv_states, ssm_states))
 
         def mix(m, h, resid, nrm, nxt):
@@ -148,12 +156,14 @@ class MambaModel(nn.Module):
                                  defer_norm=True)
             return m.step_2d(h, cs, ss, resid=resid, next_norm=nxt, defer_norm=True)
 
-        h = self._run(input_ids.reshape(-1), mix, defer_norm=True)
+        h = self._run(input_ids.reshape(-1), mix, defer_norm=True, resid=hidden)
         E = self.embeddings.weight
         if h.dim() == 2 and decode_linear_ok(h, E):
-            return decode_head_argmax(h, E, ids_out)[:, None, :]
+            return decode_head_argmax(h, E, ids_out, embed_out=hidden)[:, None, :]
         logits = self._head(h)
         argmax_rows(logits if logits.stride(-1) == 1 else logits.contiguous(), out=ids_out)
+        if hidden is not None:
+            hidden.copy_(self.embeddings(ids_out))
         return logits[:, None, :]
 
     def step(self, input_ids: torch.Tensor, conv_states, ssm_states, inplace: bool = False):

@@ -48,7 +48,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_version_and_status_names(lib):
-    assert lib.mm_abi_version() == _lib.ABI_VERSION == 5
+    assert lib.mm_abi_version() == _lib.ABI_VERSION == 6
     assert lib.mm_status_name(0) == b"MM_OK"
     assert lib.mm_status_name(-3) == b"MM_ERR_DSTATE"
     assert lib.mm_status_name(-99) == b"MM_ERR_UNKNOWN"
@@ -297,6 +297,33 @@ def test_decode_head_argmax_validation(lib):
     # narrow N (no shared-X head): mm_decode_linear's workspace, then mm_argmax_rows
     assert lib.mm_decode_head_argmax_workspace_size(4, 3072, 768) == \
         lib.mm_decode_linear_workspace_size(4, 3072, 768)
+
+
+def test_decode_head_argmax_embed_validation(lib):
+    """mm_decode_head_argmax_embed: mm_decode_head_argmax's checks plus the tied (N, K)
+    table and the (M, K) rows, both with row strides >= K, multiples of 8, 16-byte
+    aligned; all checked before any launch."""
+    def call(table=FAKE, ld_t=2560, rows=FAKE, ld_r=2560, ids=FAKE, **kw):
+        prm = _lib.LinearParams()
+        prm.x = prm.w_packed = prm.y = FAKE
+        prm.M, prm.N, prm.K = 64, 50280, 2560
+        prm.ldx, prm.ldy = 2560, 50280
+        prm.dtype, prm.epilogue = _lib.F16, 0
+        for k, v in kw.items():
+            setattr(prm, k, v)
+        return lib.mm_decode_head_argmax_embed(ctypes.byref(prm), ids, table, ld_t, rows, ld_r, None)
+    assert lib.mm_decode_head_argmax_embed(None, FAKE, FAKE, 2560, FAKE, 2560, None) == \
+        _lib.ERR_NULL_POINTER
+    assert call(table=None) == _lib.ERR_NULL_POINTER
+    assert call(rows=None) == _lib.ERR_NULL_POINTER
+    assert call(ld_t=2552) == _lib.ERR_LAYOUT
+    assert call(ld_r=2564) == _lib.ERR_LAYOUT
+    assert call(table=FAKE + 8) == _lib.ERR_LAYOUT
+    assert call(rows=FAKE + 8) == _lib.ERR_LAYOUT
+    assert call(ids=None) == _lib.ERR_NULL_POINTER     # then mm_decode_head_argmax's checks
+    assert call(epilogue=1) == _lib.ERR_SHAPE
+    assert call() == _lib.ERR_WORKSPACE
+    assert call(M=0, workspace=FAKE, workspace_bytes=1 << 30) == _lib.OK
 
 
 def test_argmax_validation(lib):

@@ -319,6 +319,13 @@ def test_decode_head_argmax(dev, M, K, N, dtype):
     assert torch.equal(logits, ref)
     assert torch.equal(ids, argmax_rows(ref))
     assert torch.equal(ids, ref.float().argmax(dim=1))
+    # with the next step's embedding rows (the head's tied table) written beside the ids
+    emb = torch.full((M, K), float("nan"), dtype=dtype, device=dev)
+    ids_e = torch.empty_like(ids)
+    lg_e = decode_head_argmax(x, w, ids_e, embed_out=emb)
+    torch.cuda.synchronize()
+    assert torch.equal(lg_e, ref) and torch.equal(ids_e, ids)
+    assert torch.equal(emb, w[ids])
     # ties: every row's winner duplicated at a lower and a higher column
     top = ids.clone()
     w2 = w.clone()
