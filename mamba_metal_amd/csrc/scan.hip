@@ -504,6 +504,11 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
       const bool full = (t0 + kT <= p.seqlen) && (d0 + CPW <= p.dim);
 
       // ---- prologue ----
+      // Wave priority: the scan phase issues ahead of the prologue / epilogue of the other
+      // workgroup sharing the SIMD (its loads and LDS round trips wait either way), which
+      // measured config 4 2.722 -> 2.646 ms and the 2.8B prefill scan 0.661 -> 0.646 ms,
+      // config 2 unchanged; reversed (prologue / epilogue first) it was slower (2.76 ms).
+      __builtin_amdgcn_s_setprio(0);
       float yskip[EPT], gate[EPT], dtv[EPT], duv[EPT];
 #pragma unroll
       for (int j = 0; j < EPT; ++j) {
@@ -554,6 +559,7 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
       }
       __syncthreads();
 
+      __builtin_amdgcn_s_setprio(2);
       // ---- scan: lane = channel (mod CPW), wave and half-wave = state group; LDS reads
       // one group ahead ----
       struct Grp {
@@ -635,6 +641,7 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
       if constexpr (MODE == kSummary) return;
 
       // ---- epilogue: y = (sum_g partial + D*u) * SiLU(z) -> HBM ----
+      __builtin_amdgcn_s_setprio(0);
       float yv[EPT];
 #pragma unroll
       for (int j = 0; j < EPT; ++j) yv[j] = yskip[j];
