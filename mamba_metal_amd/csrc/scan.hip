@@ -853,13 +853,15 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
       }
     }
     // Persistent grid size, measured on 256 CUs (three workgroups fit a CU): with two to
-    // four chains per CU, two workgroups per CU (B=4 D=5120 L=32768, 640 chains: 2.88 ms
-    // at 512 workgroups, 3.07 at 768, 3.0-3.2 at 576; B=16 D=1536 L=4096, 768 chains:
-    // 0.464 vs 0.500 ms); otherwise every resident slot -- with more chains the tickets
-    // keep three per CU evenly busy (B=8..64 x D=5120, 1280-10240 chains: 1.30-1.32 ms at
-    // 768 vs 1.46-1.47 at 512), with fewer the chains' segment order is the critical path
-    // and spare workgroups take the next segments early (B=8 D=1536 L=8192: 0.605 ms at
-    // 768, 0.627 at 512).
+    // three chains per CU, two workgroups per CU (B=4 D=5120 L=32768, 640 chains: 2.88 ms
+    // at 512 workgroups, 3.07 at 768, 3.0-3.2 at 576); otherwise every resident slot --
+    // with more chains the tickets keep three per CU evenly busy (B=8..64 x D=5120,
+    // 1280-10240 chains: 1.30-1.32 ms at 768 vs 1.46-1.47 at 512; since the scan phase
+    // runs at a raised wave priority also from three chains per CU: B=16 D=1536 L=4096,
+    // 768 chains, 0.44 -> 0.41 ms, B=7 D=4096 L=8192 0.97 -> 0.90, B=6 D=5120 L=4096 0.535
+    // -> 0.49), with fewer the chains' segment order is the critical path and spare
+    // workgroups take the next segments early (B=8 D=1536 L=8192: 0.605 ms at 768, 0.627
+    // at 512).
     // 48-channel blocks (see use_48), e.g. B=8 D=1536: 384 32-channel chains, 256
     // 48-channel ones on 256 CUs
     if (use_48(a->batch, a->dim, cus)) {
@@ -870,7 +872,7 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
       launch_chained<DT, LAYOUT, SPL, 6, VEC, 48>(p, a, s, w, r48);
       return;
     }
-    if (p.ncb >= 2 * cus && p.ncb < 4 * cus && r32 > 2 * cus) r32 = 2 * cus;
+    if (p.ncb >= 2 * cus && p.ncb < 3 * cus && r32 > 2 * cus) r32 = 2 * cus;
     launch_chained<DT, LAYOUT, SPL, GS / 2, VEC, 32>(p, a, s, w, r32);
   } else if constexpr (GS == 16) {
     // 16-channel blocks of 4 waves, one state per lane (see prefer_single_state)

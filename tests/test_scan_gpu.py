@@ -436,11 +436,11 @@ def test_split_long_sequence_160_blocks(oracle_lib, dev):
     _blockwise_parity(oracle_lib, dev, 2, 5120, 32768, seed=6)
 
 
-@pytest.mark.parametrize("dim,seqlen", [(16352, 512), (16384, 512), (32736, 256), (32768, 256)])
+@pytest.mark.parametrize("dim,seqlen", [(16352, 512), (16384, 512), (24544, 384), (24576, 384)])
 def test_grid_regime_boundaries(oracle_lib, dev, dim, seqlen):
     """Chain counts (32-channel blocks, batch 1) on either side of the persistent grid's
     switches on a 256-CU part: 511 / 512 chains (all resident slots / two workgroups per
-    CU) and 1023 / 1024 (two per CU / all slots).  One channel of every block against the
+    CU) and 767 / 768 (two per CU / all slots).  One channel of every block against the
     oracle."""
     _blockwise_parity(oracle_lib, dev, 1, dim, seqlen, seed=dim % 97)
 
