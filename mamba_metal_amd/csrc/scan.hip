@@ -166,18 +166,20 @@ inline bool use_48(int64_t batch, int64_t dim, int64_t cus) {
 }
 
 // Time-contiguous dstate 9..16 scans with 2-3 chains per CU in 16-channel blocks that
-// neither the 48-channel blocks nor the split scan take run 16-channel blocks with one
-// state per lane: three resident workgroups of 4 waves per CU then hold three chains per
-// CU (3 waves per SIMD), where 32-channel blocks leave half the CUs two chains.  Measured
-// against the 32-channel blocks (fp16, L=8192): B=1 D=8704 0.565 -> 0.500 ms, B=2 D=5120
-// 0.59 -> 0.545, B=3 D=4096 0.588 -> 0.557.  It loses where the recurrence is VALU-bound
-// or the 48-channel blocks apply, its single state per lane giving the scheduler half the
-// independent work: B=4 D=5120 L=32768 2.79 -> 3.18 ms, B=64 D=5120 L=512 0.69 -> 0.84,
-// B=8 D=1536 L=8192 0.64 (48-channel) -> 0.68.  A lane's update costs the same five VALU
+// the split scan does not take run 16-channel blocks with one state per lane: three
+// resident workgroups of 4 waves per CU then hold three chains per CU (3 waves per SIMD),
+// where 32-channel blocks leave half the CUs two chains and 48-channel blocks put 2, 2, 1,
+// 1 waves on the SIMDs.  Measured against the 32-channel blocks (fp16, L=8192): B=1 D=8704
+// 0.565 -> 0.500 ms, B=2 D=5120 0.59 -> 0.545, B=3 D=4096 0.588 -> 0.557; against the
+// 48-channel blocks at B=8 D=1536 (config 2) 0.568 -> 0.518-0.528 and 0.61 -> 0.60 on two
+// boxes (it lost, 0.64 -> 0.68, before the scan phase ran at a raised wave priority).  It
+// loses where the recurrence is VALU-bound, its single state per lane giving the scheduler
+// half the independent work: B=4 D=5120 L=32768 2.78 -> 3.24 ms, B=64 D=5120 L=512 0.68 ->
+// 0.84, B=16 D=1536 L=4096 0.43 -> 0.52.  A lane's update costs the same five VALU
 // instructions; per (channel, step) the epilogue sums 16 partial y's instead of 8.
 inline bool prefer_single_state(int64_t batch, int64_t dim, int64_t seqlen, int64_t cus) {
   const int64_t ncb16 = batch * ceil_div(dim, 16);
-  return ncb16 > 2 * cus && ncb16 <= 3 * cus && !use_48(batch, dim, cus) &&
+  return ncb16 > 2 * cus && ncb16 <= 3 * cus &&
          !split_capable(batch * ceil_div(dim, 64), kGroups16, seqlen);
 }
 

@@ -197,23 +197,23 @@ def test_layouts(oracle_lib, dev, layout, dtype):
 
 
 @pytest.mark.parametrize("layout", ["bdl", "bld"])
-def test_48_channel_blocks(oracle_lib, dev, layout):
-    """B=8 D=1536 (384 32-channel chains, 256 48-channel ones on 256 CUs) runs the 48-channel
-    blocks of 6 waves (thread t: channel t % 48, state group t / 48), time- and
-    channel-contiguous; a 300-step sequence ends inside a tile."""
+def test_48_and_16_channel_blocks(oracle_lib, dev, layout):
+    """B=8 D=1536 (384 32-channel chains, 256 48-channel ones, 768 16-channel ones on 256
+    CUs): channel-contiguous inputs run the 48-channel blocks of 6 waves (thread t: channel
+    t % 48, state group t / 48), time-contiguous ones the 16-channel blocks of one state per
+    lane; a 300-step sequence ends inside a tile."""
     inp = fp16_inputs(8, 1536, 16, 300, seed=48)
-    check(oracle_lib, dev, inp, f"48-channel blocks {layout}", dtype=torch.float16, softplus=True,
-          layout=layout)
+    check(oracle_lib, dev, inp, f"48/16-channel blocks {layout}", dtype=torch.float16,
+          softplus=True, layout=layout)
 
 
 def _single_state_dim(cus, batch):
     """A ragged dim (16 k - 8) whose time-contiguous scan runs the 16-channel blocks of one
-    state per lane on a part with `cus` CUs: 2 cus < batch * k <= 3 cus 16-channel chains,
-    more than `cus` 48-channel ones (so not the 48-channel blocks) and more than 128
-    64-channel ones (no split scan at short lengths)."""
+    state per lane on a part with `cus` CUs: 2 cus < batch * k <= 3 cus 16-channel chains
+    and more than 128 64-channel ones (no split scan at short lengths)."""
     for k in range(2 * cus // batch + 1, 3 * cus // batch + 1):
         dim = 16 * k - 8
-        if batch * -(-dim // 48) > cus and batch * -(-dim // 64) > 128:
+        if batch * -(-dim // 64) > 128:
             return dim
     pytest.skip(f"no ragged 16-channel-block shape at batch {batch} on {cus} CUs")
 
@@ -222,7 +222,7 @@ def _single_state_dim(cus, batch):
 @pytest.mark.parametrize("seqlen", [300, 301])
 def test_16_channel_blocks_ragged(oracle_lib, dev, dtype, seqlen):
     """16-channel blocks (one state per lane) with a partial last block (dim = 16 k - 8,
-    4088 at batch 3 on 256 CUs) and a sequence ending inside a tile; an odd length takes the
+    2728 at batch 3 on 256 CUs) and a sequence ending inside a tile; an odd length takes the
     element-wise (non-vector) loads.  dstate 16 and 12 (padded states)."""
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     dim = _single_state_dim(cus, 3)
