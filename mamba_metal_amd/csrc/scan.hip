@@ -801,6 +801,17 @@ void launch_chained(Params p, const mm_scan_params* a, hipStream_t s, const WsLa
   float* carry = reinterpret_cast<float*>(ws + w.carry);
   const float* bc = reinterpret_cast<const float*>(ws + w.bc);
   pick_segments(p, resident);
+  if (p.ncb <= resident && 3 * p.ncb > 2 * resident) {
+    // Every chain has a workgroup of its own and they fill most of the grid: a chain's
+    // segments could only run one after another, so one segment per chain saves the
+    // hand-offs (B=2 D=5120 L=8192, 640 16-channel chains: 0.527 -> 0.479 ms; config 2
+    // 0.596 -> 0.584; B=3 D=4096 0.529 -> 0.507).  With few chains the spare workgroups
+    // claiming the next segments early (their first loads issued before the wait) pay
+    // for the hand-offs: B=2 D=1536 L=2048, 96 chains, 0.0568 -> 0.058 ms with one segment.
+    p.seg_tiles = p.Lp / kT;
+    p.nseg = 1;
+    p.nunits = p.ncb;
+  }
   const int64_t grid = std::min<int64_t>(p.nunits, resident);
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(64 * G), 0, s, p, a->u,
                      a->delta, a->z, a->y, bc, a->state_out, ctl, carry, ctl, nullptr);
