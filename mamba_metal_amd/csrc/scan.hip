@@ -303,7 +303,11 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
   // tiles here saves 9 KB of LDS and measured ~3% faster at config 4.
   constexpr int YT = CPW * kT;
   static_assert(kT / 4 >= 8, "the chunk permutation needs eight chunks per row");
-  __shared__ __attribute__((aligned(16))) float s_y[GS][YT];
+  // 16-channel blocks along time fold their four quarter-waves' partial y's in registers
+  // (the quarters are the wave's four 16-lane rows): one partial per wave is stored.
+  constexpr bool FOLD4 = CPW == 16 && LAYOUT == kTimeContig && MODE != kSummary;
+  constexpr int YG = FOLD4 ? G : GS;
+  __shared__ __attribute__((aligned(16))) float s_y[YG][YT];
   auto aty = [](int c, int t) {
     return (LAYOUT == kTimeContig) ? c * kT + ((((t >> 2) ^ (c & 7)) << 2) | (t & 3))
                                    : t * CPW + c;
@@ -632,7 +636,21 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
           }
           ys[j] = acc;
         }
-        if constexpr (LAYOUT == kTimeContig) {
+        if constexpr (FOLD4) {
+          // sum over the wave's four rows (quarters, state groups g, g+G, g+2G, g+3G) of
+          // steps tt..tt+3: the 32-lane swaps add rows r and r+2 (steps 0 and 2 stay in
+          // the lower half, 1 and 3 in the upper), the 16-lane swap then rows r and r+1;
+          // row q ends with step tt+q's sum, (q0 + q2) + (q1 + q3)
+          const auto a02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ys[0]), __float_as_uint(ys[2]),
+                                                            false, false);
+          const auto a13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ys[1]), __float_as_uint(ys[3]),
+                                                            false, false);
+          const float s02 = __uint_as_float(a02[0]) + __uint_as_float(a02[1]);
+          const float s13 = __uint_as_float(a13[0]) + __uint_as_float(a13[1]);
+          const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(s02), __float_as_uint(s13),
+                                                          false, false);
+          s_y[g][aty(lch, tt + (lane >> 4))] = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+        } else if constexpr (LAYOUT == kTimeContig) {
           *reinterpret_cast<float4*>(&s_y[sg][aty(lch, tt)]) = make_float4(ys[0], ys[1], ys[2], ys[3]);
         } else {
 #pragma unroll
@@ -649,15 +667,15 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
       for (int j = 0; j < EPT; ++j) yv[j] = yskip[j];
       {
         // all G partial reads in flight before the (in-order) sum
-        FV part[GS][EPT / VW];
+        FV part[YG][EPT / VW];
 #pragma unroll
-        for (int gg = 0; gg < GS; ++gg)
+        for (int gg = 0; gg < YG; ++gg)
 #pragma unroll
           for (int j = 0; j < EPT; j += VW)
             part[gg][j / VW] = *reinterpret_cast<const FV*>(
                 &s_y[gg][(LAYOUT == kTimeContig) ? aty(vc, vt + j) : aty(vc + j, vt)]);
 #pragma unroll
-        for (int gg = 0; gg < GS; ++gg)
+        for (int gg = 0; gg < YG; ++gg)
 #pragma unroll
           for (int j = 0; j < EPT; j += VW)
 #pragma unroll
@@ -891,7 +909,8 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
     // 16-channel blocks of 4 waves, one state per lane (see prefer_single_state)
     auto k16 = scan_kernel<DT, LAYOUT, SPL, 4, VEC, kChained, 16>;
     static DeviceCache c16_cache;
-    const int64_t r16 = cus * resident_per_cu(c16_cache, k16, 256);
+    // three per CU at most: the measured regime (with the folded partial y's four fit)
+    const int64_t r16 = cus * std::min<int64_t>(3, resident_per_cu(c16_cache, k16, 256));
     set_blocks(p, a->batch, 16);
     launch_chained<DT, LAYOUT, SPL, 4, VEC, 16>(p, a, s, w, r16);
   } else {
