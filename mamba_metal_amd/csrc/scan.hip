@@ -159,7 +159,9 @@ inline void pick_shape(int64_t dstate, int* groups, int* spl) {
 // Between one and two 32-channel chains per CU half the CUs would run two chains, which
 // then set the critical path.  48-channel blocks of 6 waves make it one chain per CU where
 // that many fit; their carries fit the workspace's 64-channel layout when dim rounds up
-// no further for 48 than for 64.
+// no further for 48 than for 64.  Time-contiguous inputs in this range take the 16-channel
+// blocks instead (prefer_single_state is checked first), so these serve channel-contiguous
+// ones.
 inline bool use_48(int64_t batch, int64_t dim, int64_t cus) {
   return batch * ceil_div(dim, 32) > cus && batch * ceil_div(dim, 48) <= cus &&
          round_up(dim, 48) <= round_up(dim, 64);
@@ -176,7 +178,8 @@ inline bool use_48(int64_t batch, int64_t dim, int64_t cus) {
 // loses where the recurrence is VALU-bound, its single state per lane giving the scheduler
 // half the independent work: B=4 D=5120 L=32768 2.78 -> 3.24 ms, B=64 D=5120 L=512 0.68 ->
 // 0.84, B=16 D=1536 L=4096 0.43 -> 0.52.  A lane's update costs the same five VALU
-// instructions; per (channel, step) the epilogue sums 16 partial y's instead of 8.
+// instructions; each wave folds its four rows' partial y's in registers (see FOLD4), so
+// the epilogue sums 4 partials per (channel, step) instead of 8.
 inline bool prefer_single_state(int64_t batch, int64_t dim, int64_t seqlen, int64_t cus) {
   const int64_t ncb16 = batch * ceil_div(dim, 16);
   return ncb16 > 2 * cus && ncb16 <= 3 * cus &&
@@ -511,9 +514,11 @@ __global__ __launch_bounds__(64 * G, 1) void scan_kernel(
 
       // ---- prologue ----
       // Wave priority: the scan phase issues ahead of the prologue / epilogue of the other
-      // workgroup sharing the SIMD (its loads and LDS round trips wait either way), which
-      // measured config 4 2.722 -> 2.646 ms and the 2.8B prefill scan 0.661 -> 0.646 ms,
-      // config 2 unchanged; reversed (prologue / epilogue first) it was slower (2.76 ms).
+      // workgroups sharing the SIMD (their loads and LDS round trips wait either way),
+      // which measured config 4 2.722 -> 2.646 ms and the 2.8B prefill scan 0.661 -> 0.646
+      // ms (config 2 on the 48-channel blocks unchanged; on the 16-channel blocks, three
+      // waves per SIMD, it turned a loss into a gain: see prefer_single_state); reversed
+      // (prologue / epilogue first) it was slower (2.76 ms).
       __builtin_amdgcn_s_setprio(0);
       float yskip[EPT], gate[EPT], dtv[EPT], duv[EPT];
 #pragma unroll
