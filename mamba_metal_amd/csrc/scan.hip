@@ -167,11 +167,14 @@ inline bool use_48(int64_t batch, int64_t dim, int64_t cus) {
          round_up(dim, 48) <= round_up(dim, 64);
 }
 
-// Time-contiguous dstate 9..16 scans with 2-3 chains per CU in 16-channel blocks that
-// the split scan does not take run 16-channel blocks with one state per lane: three
-// resident workgroups of 4 waves per CU then hold three chains per CU (3 waves per SIMD),
-// where 32-channel blocks leave half the CUs two chains and 48-channel blocks put 2, 2, 1,
-// 1 waves on the SIMDs.  Measured against the 32-channel blocks (fp16, L=8192): B=1 D=8704
+// Time-contiguous dstate 9..16 scans with 2-4 (not exactly 4) chains per CU in 16-channel
+// blocks that the split scan does not take run 16-channel blocks with one state per lane:
+// three or four resident workgroups of 4 waves per CU then hold three or four chains per
+// CU, where 32-channel blocks leave some CUs one chain fewer and 48-channel blocks put 2,
+// 2, 1, 1 waves on the SIMDs.  (At exactly 4 per CU the 32-channel blocks are even, 2 per
+// CU, and faster: B=4 D=4096 L=8192 0.64 vs 0.69 ms; from 3 to 4 per CU the 16-channel
+// blocks gained 3-9%: B=7 D=2048 0.638 -> 0.60 ms, B=5 D=3072 0.649 -> 0.61, B=2 D=7680
+// 0.647 -> 0.59, B=3 D=5120 0.70 -> 0.68.)  Measured against the 32-channel blocks (fp16, L=8192): B=1 D=8704
 // 0.565 -> 0.500 ms, B=2 D=5120 0.59 -> 0.545, B=3 D=4096 0.588 -> 0.557; against the
 // 48-channel blocks at B=8 D=1536 (config 2) 0.568 -> 0.518-0.528 and 0.61 -> 0.60 on two
 // boxes (it lost, 0.64 -> 0.68, before the scan phase ran at a raised wave priority).  It
@@ -182,7 +185,7 @@ inline bool use_48(int64_t batch, int64_t dim, int64_t cus) {
 // the epilogue sums 4 partials per (channel, step) instead of 8.
 inline bool prefer_single_state(int64_t batch, int64_t dim, int64_t seqlen, int64_t cus) {
   const int64_t ncb16 = batch * ceil_div(dim, 16);
-  return ncb16 > 2 * cus && ncb16 <= 3 * cus &&
+  return ncb16 > 2 * cus && ncb16 < 4 * cus &&
          !split_capable(batch * ceil_div(dim, 64), kGroups16, seqlen);
 }
 
@@ -914,9 +917,10 @@ void launch_k(Params p, const mm_scan_params* a, hipStream_t s, const WsLayout& 
     // 16-channel blocks of 4 waves, one state per lane (see prefer_single_state)
     auto k16 = scan_kernel<DT, LAYOUT, SPL, 4, VEC, kChained, 16>;
     static DeviceCache c16_cache;
-    // three per CU at most: the measured regime (with the folded partial y's four fit)
-    const int64_t r16 = cus * std::min<int64_t>(3, resident_per_cu(c16_cache, k16, 256));
+    // three workgroups per CU up to three chains per CU, four above (the folded partial
+    // y's keep a workgroup at 17.7 KB of LDS, so four fit)
     set_blocks(p, a->batch, 16);
+    const int64_t r16 = cus * std::min<int64_t>(p.ncb > 3 * cus ? 4 : 3, resident_per_cu(c16_cache, k16, 256));
     launch_chained<DT, LAYOUT, SPL, 4, VEC, 16>(p, a, s, w, r16);
   } else {
     auto kern = scan_kernel<DT, LAYOUT, SPL, GS, VEC, kChained, 64>;

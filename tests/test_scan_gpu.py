@@ -451,6 +451,13 @@ def test_bf16_large_every_block(oracle_lib, dev):
     _blockwise_parity(oracle_lib, dev, 2, 5120, 8192, seed=7, dtype=torch.bfloat16)
 
 
+def test_16_channel_blocks_four_per_cu_every_block(oracle_lib, dev):
+    """B=7 D=2048 L=2048 fp16 (896 16-channel chains: between 3 and 4 per CU on 256 CUs, so
+    four workgroups per CU, one segment each): one channel of every block against the
+    oracle."""
+    _blockwise_parity(oracle_lib, dev, 7, 2048, 2048, seed=27)
+
+
 def test_16_channel_blocks_full_length_every_block(oracle_lib, dev):
     """B=1 D=8704 L=8192 fp16 (544 16-channel chains of one state per lane on 256 CUs, four
     segment hand-offs each): one channel of every block against the oracle."""
